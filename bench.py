@@ -1,0 +1,365 @@
+"""Benchmark of the MI355X scan on the reference's headline workload.
+
+Default (what the driver runs): ``python bench.py`` -> one GPU, workload C4 of the
+reference's north star: pscan forward + backward on (batch 8, dim 1024, seqlen 65536) bf16,
+synthetic Mamba-style inputs (gates = exp(-softplus(N(0,1)) * U[0.001, 0.1]),
+tokens = 0.1 N(0,1), grad_out = N(0,1)), resident in HBM before timing starts.
+
+One step = ``pscan(gates, tokens)`` + ``torch.autograd.grad`` of it with ``grad_out``: the
+forward kernel and the fused backward kernel. Algorithmic bytes per step, N = B*D*L and s =
+itemsize (eval/benchmark.py:62-65 counts the forward the same way):
+    forward  3*N*s  (read gates, tokens; write out)
+    backward 5*N*s  (read gates, out, grad_out; write grad_gates, grad_tokens)
+    step     8*N*s
+``value`` = step bytes / (bracketed wall time of K steps / K), in GB/s. ``roofline`` is the
+backward kernel (the dominant one), timed alone with HIP events on the stream it runs on.
+``cpu_baseline`` times the reference's CPU path -- Hillis-Steele ``parallel_scan_torch``
+forward plus the PScan.backward composition -- on a bounded sample of rows of the same
+inputs, on the host cores.
+
+Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen sweep, forward
+and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant). Multi-GPU runs are not part
+of this build: ``--gpus N`` with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published peak
+
+DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+SHORT = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+# workload -> (batch, dim, seqlen, dtype, input distribution)
+WORKLOADS = {
+    "c1": (2, 256, 1024, "float32", "uniform"),
+    "c3": (4, 512, 8192, "bfloat16", "uniform"),
+    "c4": (8, 1024, 65536, "bfloat16", "mamba"),
+    "c5": (64, 4096, 256, "float32", "sigmoid"),
+}
+C2_SEQLENS = [2 ** k for k in range(5, 17)]
+METRIC = "fwd+bwd scan GB/s and % HBM peak; p50 ms at B8 D1024 L65536 bf16"
+
+
+def make_inputs(batch, dim, seqlen, dtype, dist, seed=0, device="cuda", grad=True):
+    """Seeded synthetic inputs of one workload: (gates, tokens, grad_out or None), contiguous
+    (batch, dim, seqlen) tensors of ``dtype``, drawn in fp32 then rounded."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    shape = (batch, dim, seqlen)
+
+    def rand():
+        return torch.rand(shape, generator=gen, device=device)
+
+    def randn():
+        return torch.randn(shape, generator=gen, device=device)
+
+    if dist == "uniform":  # configs 1-3
+        gates = 0.99 + 0.01 * rand()
+        tokens = randn() / seqlen
+    elif dist == "mamba":  # config 4
+        dt = 0.001 + 0.099 * rand()
+        gates = torch.exp(-torch.nn.functional.softplus(randn()) * dt)
+        del dt
+        tokens = 0.1 * randn()
+    elif dist == "sigmoid":  # config 5
+        gates = torch.sigmoid(2.0 + randn())
+        tokens = randn()
+    else:
+        raise ValueError(dist)
+    grad_out = randn().to(dtype).contiguous() if grad else None
+    return gates.to(dtype).contiguous(), tokens.to(dtype).contiguous(), grad_out
+
+
+# ------------------------------------------------------------------------------ timing
+def _events(n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def time_each(fn, warmup, iters):
+    """Per-call durations (ms) from HIP event pairs on the current stream (the stream every
+    fpscan kernel is launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts, ends = _events(iters), _events(iters)
+    for i in range(iters):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def percentile(xs, q):
+    s = sorted(xs)
+    if not s:
+        return float("nan")
+    k = (len(s) - 1) * q
+    lo, hi = math.floor(k), math.ceil(k)
+    return s[lo] + (s[hi] - s[lo]) * (k - lo)
+
+
+# ------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline(gates, tokens, grad_out, target_s):
+    """Reference CPU path (Hillis-Steele forward + PScan.backward composition with the
+    Hillis-Steele reverse scan) on the first rows of the inputs, sized to about target_s."""
+    import oracle  # the cpu_baseline leg is the one place bench.py uses the oracle package
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    B, D, L = gates.shape
+    rows_total = B * D
+    s = gates.element_size()
+
+    def run(rows):
+        g = gates.reshape(rows_total, L)[:rows].cpu()
+        x = tokens.reshape(rows_total, L)[:rows].cpu()
+        go = grad_out.reshape(rows_total, L)[:rows].cpu()
+        t0 = time.perf_counter()
+        y = oracle.parallel_scan_torch(g, x)
+        oracle.pscan_backward_composed(g, y, go, oracle.parallel_scan_torch)
+        return time.perf_counter() - t0
+
+    rows = 1
+    dt = run(rows)
+    while dt < 0.5 and rows < rows_total:  # grow until one run is measurable
+        rows = min(rows_total, rows * 4)
+        dt = run(rows)
+    rows = max(1, min(rows_total, int(rows * max(1.0, target_s / 3 / max(dt, 1e-6)))))
+    times = [run(rows) for _ in range(3)]
+    p50 = statistics.median(times)
+    gbps = 8 * rows * L * s / p50 / 1e9
+    return {
+        "value": round(gbps, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{rows} of {rows_total} rows x {L} {SHORT[gates.dtype]}: Hillis-Steele "
+                  f"forward + composed backward (eval/baselines.py:40-61, fpscan/ops.py:69-83), "
+                  f"p50 of 3 runs ({p50:.2f} s each)",
+        "cpu_model": platform.processor() or _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def load_traffic(workload, dtype_short):
+    """HBM bytes per backward launch measured by rocprofv3 PMC counters (FETCH_SIZE,
+    WRITE_SIZE, scaled by a copy kernel of known size), committed under profiles/."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"pmc_traffic_{workload}_{dtype_short}.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return d.get("bwd_bytes_per_launch"), os.path.relpath(path)
+    except (OSError, ValueError):
+        return None, None
+
+
+# ------------------------------------------------------------------------------ workloads
+def bench_headline(args):
+    import fpscan_amd
+
+    B, D, L, dname, dist = WORKLOADS[args.workload]
+    dtype = DTYPES[args.dtype or dname]
+    N = B * D * L
+    s = torch.empty((), dtype=dtype).element_size()
+    gates, tokens, grad_out = make_inputs(B, D, L, dtype, dist, seed=0)
+    g = gates.clone().requires_grad_()
+    x = tokens.clone().requires_grad_()
+
+    def step():
+        out = fpscan_amd.pscan(g, x)
+        return torch.autograd.grad(out, (g, x), grad_out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # K timed steps, bracketed by a synchronisation on both sides (one process, one GPU)
+    start, end = _events(2)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    step_p = time_each(step, 1, args.steps)
+
+    # kernels alone
+    out = torch.empty_like(tokens)
+    gg = torch.empty_like(gates)
+    gx = torch.empty_like(gates)
+    fwd_t = time_each(lambda: fpscan_amd.scan_forward(gates, tokens, out=out), 2, args.steps)
+    y = fpscan_amd.scan_forward(gates, tokens)
+    bwd_t = time_each(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx), 2,
+                      args.steps)
+    fwd_avg, bwd_avg = statistics.mean(fwd_t), statistics.mean(bwd_t)
+    bwd_bytes = 5 * N * s
+    achieved = bwd_bytes / (bwd_avg / 1e3) / 1e9
+    traffic, traffic_src = load_traffic(args.workload, SHORT[dtype])
+    value = 8 * N * s / (ms_per_step / 1e3) / 1e9
+
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": SHORT[dtype],
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: pscan fwd+bwd B{B} D{D} L{L} {SHORT[dtype]}",
+            "batch": B, "dim": D, "seqlen": L, "inputs": dist,
+            "parallelism": "none (1 GPU; rows independent)",
+        },
+        "p50_ms": round(percentile(step_p, 0.5), 5),
+        "p90_ms": round(percentile(step_p, 0.9), 5),
+        "hbm_frac": round(value / HBM_PEAK_GBPS, 4),
+        "fwd_kernel": {"avg_ms": round(fwd_avg, 5), "p50_ms": round(percentile(fwd_t, 0.5), 5),
+                       "gbps": round(3 * N * s / (fwd_avg / 1e3) / 1e9, 1)},
+        "bwd_kernel": {"avg_ms": round(bwd_avg, 5), "p50_ms": round(percentile(bwd_t, 0.5), 5),
+                       "gbps": round(achieved, 1)},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "scan_long_rows<bwd> (fused backward)",
+            "algorithmic_bytes_per_launch": bwd_bytes,
+            "traffic_source": traffic_src,
+        },
+        "wall_ms_timed_region": round(wall_ms, 3),
+        "device": torch.cuda.get_device_name(),
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(gates, tokens, grad_out, args.cpu_seconds)
+    else:
+        res["cpu_baseline"] = None
+    return res
+
+
+def bench_sweep(args):
+    """Config 2: fp32 B2 D256 forward and reverse scan_forward over seqlen 32..65536
+    (eval/benchmark.py's table: p50/p90 ms and GB/s = 3*N*s / p50)."""
+    import fpscan_amd
+
+    rows = []
+    for L in C2_SEQLENS:
+        gates, tokens, _ = make_inputs(2, 256, L, torch.float32, "uniform", seed=L, grad=False)
+        out = torch.empty_like(tokens)
+        for rev in (False, True):
+            t = time_each(lambda: fpscan_amd.scan_forward(gates, tokens, rev, out), 10, args.iters)
+            p50 = percentile(t, 0.5)
+            rows.append({"seqlen": L, "reverse": rev, "p50_ms": round(p50, 5),
+                         "p90_ms": round(percentile(t, 0.9), 5),
+                         "gbps": round(3 * 2 * 256 * L * 4 / (p50 / 1e3) / 1e9, 1)})
+            print(json.dumps(rows[-1]), flush=True)
+    return {"workload": "c2: fp32 B2 D256 forward/reverse sweep", "rows": rows}
+
+
+def bench_shape(args):
+    """c1 / c3 / c5: forward, reverse and backward kernels alone, p50 over --iters."""
+    import fpscan_amd
+
+    B, D, L, dname, dist = WORKLOADS[args.workload]
+    dtypes = [DTYPES[args.dtype]] if args.dtype else (
+        [torch.bfloat16, torch.float16] if args.workload == "c3" else [DTYPES[dname]])
+    res = {"workload": args.workload, "shape": [B, D, L], "results": []}
+    for dtype in dtypes:
+        s = torch.empty((), dtype=dtype).element_size()
+        N = B * D * L
+        gates, tokens, grad_out = make_inputs(B, D, L, dtype, dist, seed=1)
+        out = torch.empty_like(tokens)
+        y = fpscan_amd.scan_forward(gates, tokens)
+        gg, gx = torch.empty_like(gates), torch.empty_like(gates)
+        entry = {"dtype": SHORT[dtype]}
+        for name, fn, nbytes in (
+            ("fwd", lambda: fpscan_amd.scan_forward(gates, tokens, False, out), 3 * N * s),
+            ("rev", lambda: fpscan_amd.scan_forward(gates, tokens, True, out), 3 * N * s),
+            ("bwd", lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx), 5 * N * s),
+        ):
+            t = time_each(fn, 5, args.iters)
+            p50 = percentile(t, 0.5)
+            entry[name] = {"p50_ms": round(p50, 5), "gbps": round(nbytes / (p50 / 1e3) / 1e9, 1)}
+        if args.workload == "c5":
+            # (batch, seqlen, dim) data: transpose in, scan, transpose out (README.md:94-99)
+            gt = gates.mT.contiguous()
+            xt = tokens.mT.contiguous()
+
+            def e2e():
+                return fpscan_amd.scan_forward(gt.mT.contiguous(), xt.mT.contiguous()).mT.contiguous()
+
+            t = time_each(e2e, 3, args.iters)
+            entry["fwd_via_mT"] = {"p50_ms": round(percentile(t, 0.5), 5)}
+        res["results"].append(entry)
+        print(json.dumps(entry), flush=True)
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--dtype", choices=list(DTYPES), default=None)
+    ap.add_argument("--iters", type=int, default=100)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--launch", default=None, help="waves_per_row,ring_depth override")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); rows are independent, so N GPUs would each run the "
+              "same kernel on 1/N of the rows with no communication.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    if args.launch:
+        import fpscan_amd.ops as ops
+
+        w, u = (int(v) for v in args.launch.split(","))
+        ops.set_launch_override(w, u)
+
+    if args.workload == "c4":
+        res = bench_headline(args)
+    elif args.workload == "c2":
+        res = bench_sweep(args)
+    else:
+        res = bench_shape(args)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,143 @@
+// fpscan_amd._C: the torch-facing module over the C ABI in include/fpscan_hip.h.
+//
+// Reference interface mirrored (saeeddhqan/fpscan):
+//   csrc/main.cpp:7-11           module with "fullscan_forward" (same name, same arguments,
+//                                returns `out`)
+//   csrc/full_scan/full_scan.h:7-36   CHECK_INPUT on Ax/Bx (same RuntimeError messages)
+//   csrc/full_scan/full_scan.cu:179-258  stride/dtype checks, tile table, launch on the
+//                                current stream
+// Added: `fullscan_backward`, the fused backward that replaces the composition in
+// fpscan/ops.py:69-83, plus the checks the reference leaves out (shapes, `out`, device).
+// Every check runs before any HIP call, so a bad call raises RuntimeError on any machine.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <string>
+
+#include "fpscan_hip.h"
+
+namespace {
+
+void check_input(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.device().is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  const auto st = t.scalar_type();
+  TORCH_CHECK(st == at::kHalf || st == at::kBFloat16 || st == at::kFloat, name,
+              " must be float16 or bfloat16 or float32");
+  TORCH_CHECK(t.dim() == 3, name, " must be a 3-d (batch, dim, seqlen) tensor, got ", t.dim(),
+              " dims");
+}
+
+void check_like(const at::Tensor& t, const at::Tensor& ref, const char* name,
+                const char* ref_name) {
+  TORCH_CHECK(t.scalar_type() == ref.scalar_type(), name, " must have the dtype of ", ref_name,
+              " (", ref.scalar_type(), "), got ", t.scalar_type());
+  TORCH_CHECK(t.sizes() == ref.sizes(), name, " must have the shape of ", ref_name, " ",
+              ref.sizes(), ", got ", t.sizes());
+  TORCH_CHECK(t.device() == ref.device(), name, " must be on ", ref.device(), ", got ",
+              t.device());
+}
+
+int dtype_code(at::ScalarType st) {
+  switch (st) {
+    case at::kFloat: return FPSCAN_DTYPE_F32;
+    case at::kHalf: return FPSCAN_DTYPE_F16;
+    default: return FPSCAN_DTYPE_BF16;
+  }
+}
+
+void check_seqlen(int64_t seqlen) {
+  TORCH_CHECK(seqlen >= 32 && seqlen <= 65536 && (seqlen & (seqlen - 1)) == 0,
+              "seqlen must be a power of 2, >= 32, <= 65536, got ", seqlen);
+}
+
+void check_status(int status) {
+  TORCH_CHECK(status == FPSCAN_OK, "fpscan: ", fpscan_strerror(status), " (status ", status,
+              ")");
+}
+
+at::Tensor fullscan_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tensor& out,
+                            bool reverse) {
+  check_input(Ax, "Ax");
+  check_input(Bx, "Bx");
+  check_like(Ax, Bx, "Ax", "Bx");
+  check_input(out, "out");
+  check_like(out, Bx, "out", "Bx");
+  check_seqlen(Bx.size(2));
+  if (Bx.numel() == 0) return out;
+
+  c10::hip::HIPGuard guard(Bx.device());
+  void* stream = c10::hip::getCurrentHIPStream(Bx.device().index()).stream();
+  // contiguous (batch, dim, seqlen): the packed strides (torch may report any stride for a
+  // size-1 dimension of a contiguous tensor)
+  const int64_t L = Bx.size(2), D = Bx.size(1);
+  const int status = fpscan_scan_fwd(Ax.data_ptr(), Bx.data_ptr(), out.data_ptr(), Bx.size(0),
+                                     D, L, D * L, L,
+                                     dtype_code(Bx.scalar_type()), reverse ? 1 : 0, nullptr, 0,
+                                     stream);
+  check_status(status);
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor> fullscan_backward(const at::Tensor& gates,
+                                                     const at::Tensor& out,
+                                                     const at::Tensor& grad_out,
+                                                     const at::Tensor& grad_gates,
+                                                     const at::Tensor& grad_tokens) {
+  check_input(gates, "gates");
+  check_input(out, "out");
+  check_input(grad_out, "grad_out");
+  check_input(grad_gates, "grad_gates");
+  check_input(grad_tokens, "grad_tokens");
+  check_like(out, gates, "out", "gates");
+  check_like(grad_out, gates, "grad_out", "gates");
+  check_like(grad_gates, gates, "grad_gates", "gates");
+  check_like(grad_tokens, gates, "grad_tokens", "gates");
+  check_seqlen(gates.size(2));
+  if (gates.numel() == 0) return {grad_gates, grad_tokens};
+  // the kernel reads neighbouring rows' boundary values (gates[t+1], out[t-1]) while other
+  // waves write, so no output may share memory with an input or with the other output
+  for (const at::Tensor* o : {&grad_gates, &grad_tokens}) {
+    for (const at::Tensor* i : {&gates, &out, &grad_out}) {
+      TORCH_CHECK(o->data_ptr() != i->data_ptr(), "fullscan_backward outputs must not alias "
+                  "its inputs");
+    }
+  }
+  TORCH_CHECK(grad_gates.data_ptr() != grad_tokens.data_ptr(),
+              "grad_gates and grad_tokens must be distinct");
+
+  c10::hip::HIPGuard guard(gates.device());
+  void* stream = c10::hip::getCurrentHIPStream(gates.device().index()).stream();
+  const int status = fpscan_scan_bwd(gates.data_ptr(), out.data_ptr(), grad_out.data_ptr(),
+                                     grad_gates.data_ptr(), grad_tokens.data_ptr(),
+                                     gates.size(0), gates.size(1), gates.size(2),
+                                     gates.size(1) * gates.size(2), gates.size(2),
+                                     dtype_code(gates.scalar_type()), nullptr, 0, stream);
+  check_status(status);
+  return {grad_gates, grad_tokens};
+}
+
+int set_launch_override(int waves_per_row, int ring_depth) {
+  const int status = fpscan_set_launch_override(waves_per_row, ring_depth);
+  TORCH_CHECK(status == FPSCAN_OK, "waves_per_row must be one of 0,1,2,4,8,16 and ring_depth "
+              "one of 0,1,2,4");
+  return status;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("fullscan_forward", &fullscan_forward,
+        "first-order linear-recurrence scan, forward or reverse, written into out (HIP, gfx950)",
+        pybind11::arg("Ax"), pybind11::arg("Bx"), pybind11::arg("out"), pybind11::arg("reverse"));
+  m.def("fullscan_backward", &fullscan_backward,
+        "fused backward of the forward scan: (grad_gates, grad_tokens) (HIP, gfx950)",
+        pybind11::arg("gates"), pybind11::arg("out"), pybind11::arg("grad_out"),
+        pybind11::arg("grad_gates"), pybind11::arg("grad_tokens"));
+  m.def("set_launch_override", &set_launch_override,
+        "tuning hook: force waves per row / ring depth (0 = built-in choice)",
+        pybind11::arg("waves_per_row"), pybind11::arg("ring_depth"));
+  m.def("abi_version", []() { return fpscan_abi_version(); });
+}

@@ -1,0 +1,771 @@
+// First-order linear-recurrence scan for MI355X (gfx950, wave64), behind the C ABI in
+// include/fpscan_hip.h.
+//
+//   y[t] = gates[t] * y[t-1] + tokens[t]          (forward; reverse runs t = L-1 .. 0)
+//
+// Reference kernel replaced: csrc/full_scan/full_scan.cu:50-177 (blocked 3-level scan,
+// 32-lane warps, 3 barriers per chunk, carry through shared memory) and its launcher
+// full_scan.cu:179-258. The backward composition of fpscan/ops.py:69-83 is fused into one
+// kernel here.
+//
+// Work decomposition
+//   A "sub-chunk" is 64 lanes x one 16-byte vector per lane per tensor: 256 fp32 or 512
+//   fp16/bf16 consecutive elements of one row. Every global load/store instruction of a
+//   wave therefore covers one contiguous 1 KiB span.
+//   Long rows (seqlen >= one sub-chunk): W waves (1..16) own a row and walk its sub-chunks
+//   in rounds of W; wave w takes sub-chunk r*W+w of round r. A ring of U sub-chunks per wave
+//   is kept in flight (loads for round r+U are issued as round r is retired). The carry
+//   between rounds is a wave-uniform fp32 value; with W > 1 the W sub-chunk aggregates of a
+//   round are exchanged through 2 x W x 8 bytes of LDS and one barrier.
+//   Short rows (seqlen < one sub-chunk): each wave holds 64/G whole rows of G lanes and runs
+//   a segmented wave scan; no carry.
+//
+// Per sub-chunk, per lane (V elements, processing order):
+//   phase 1  lane aggregate (A, B) = composition of the lane's V affine maps y -> a*y + b;
+//   scan     inclusive wave scan of the lane aggregates with DPP row_shr 1/2/4/8 and
+//            row_bcast 15/31; identity (1, 0) enters through DPP's `old` operand;
+//   carry    value entering the lane = wave_shr:1 of (B + A * c_in), lane 0 takes c_in;
+//   phase 2  the lane's V elements re-run serially from that value: y = fma(a, y, b).
+// All arithmetic is fp32; half types are widened exactly on load and rounded to nearest
+// even once on store.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <atomic>
+
+#include "fpscan_hip.h"
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------------------
+// Element types: V elements per 16-byte vector, exact widening, round-to-nearest-even
+// narrowing (the reference's to_float/from_float, csrc/full_scan/conversion.h:7-13).
+// ---------------------------------------------------------------------------------------
+struct F32 {
+  static constexpr int V = 4;
+  static constexpr int kSize = 4;
+  // default sub-chunks in flight per wave (W == 1): the deepest ring that keeps the
+  // forward / backward kernel within 64 VGPRs, i.e. 8 waves per SIMD
+  static constexpr int kRingFwd = 4;
+  static constexpr int kRingBwd = 2;
+  __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
+  }
+  __device__ static __forceinline__ u32x4 pack(const float (&f)[V]) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __float_as_uint(f[i]);
+    return v;
+  }
+};
+
+struct F16 {
+  static constexpr int V = 8;
+  static constexpr int kSize = 2;
+  // default sub-chunks in flight per wave (W == 1): the deepest ring that keeps the
+  // forward / backward kernel within 64 VGPRs, i.e. 8 waves per SIMD
+  static constexpr int kRingFwd = 4;
+  static constexpr int kRingBwd = 2;
+  __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 h = __builtin_bit_cast(f16x2, v[i]);
+      f[2 * i] = static_cast<float>(h.x);
+      f[2 * i + 1] = static_cast<float>(h.y);
+    }
+  }
+  __device__ static __forceinline__ u32x4 pack(const float (&f)[V]) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f16x2 h;
+      h.x = static_cast<_Float16>(f[2 * i]);  // v_cvt_f16_f32: round to nearest even
+      h.y = static_cast<_Float16>(f[2 * i + 1]);
+      v[i] = __builtin_bit_cast(unsigned int, h);
+    }
+    return v;
+  }
+  __device__ static __forceinline__ float widen16(unsigned short bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+  }
+};
+
+struct BF16 {
+  static constexpr int V = 8;
+  static constexpr int kSize = 2;
+  // default sub-chunks in flight per wave (W == 1): the deepest ring that keeps the
+  // forward / backward kernel within 64 VGPRs, i.e. 8 waves per SIMD
+  static constexpr int kRingFwd = 2;
+  static constexpr int kRingBwd = 1;
+  __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(v[i] << 16);
+      f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+    }
+  }
+  __device__ static __forceinline__ u32x4 pack(const float (&f)[V]) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x2 x;
+      x.x = f[2 * i];
+      x.y = f[2 * i + 1];
+      // v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN
+      v[i] = __builtin_bit_cast(unsigned int, __builtin_convertvector(x, bf16x2));
+    }
+    return v;
+  }
+  __device__ static __forceinline__ float widen16(unsigned short bits) {
+    return __uint_as_float((unsigned int)bits << 16);
+  }
+};
+
+// ---------------------------------------------------------------------------------------
+// Wave64 lane movement (DPP). Lanes whose source is outside the row / wave, or whose row is
+// masked off, keep `old`.
+// ---------------------------------------------------------------------------------------
+constexpr int kRowShr1 = 0x111;
+constexpr int kRowShr2 = 0x112;
+constexpr int kRowShr4 = 0x114;
+constexpr int kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142;
+constexpr int kRowBcast31 = 0x143;
+constexpr int kWaveShl1 = 0x130;
+constexpr int kWaveShr1 = 0x138;
+
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float dpp(float old, float src) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
+                                         kCtrl, kRowMask, 0xf, false));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// (A, B) := (earlier) o (A, B): the earlier lane's map is applied first.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ void combine_from(float& A, float& B) {
+  const float pA = dpp<kCtrl, kRowMask>(1.0f, A);
+  const float pB = dpp<kCtrl, kRowMask>(0.0f, B);
+  B = fmaf(pB, A, B);
+  A = pA * A;
+}
+
+// Same, but lanes with !ok combine with the identity (segments narrower than a DPP row).
+template <int kCtrl>
+__device__ __forceinline__ void combine_from_masked(float& A, float& B, bool ok) {
+  float pA = dpp<kCtrl>(1.0f, A);
+  float pB = dpp<kCtrl>(0.0f, B);
+  pA = ok ? pA : 1.0f;
+  pB = ok ? pB : 0.0f;
+  B = fmaf(pB, A, B);
+  A = pA * A;
+}
+
+// Inclusive scan over all 64 lanes.
+__device__ __forceinline__ void wave_scan(float& A, float& B) {
+  combine_from<kRowShr1>(A, B);
+  combine_from<kRowShr2>(A, B);
+  combine_from<kRowShr4>(A, B);
+  combine_from<kRowShr8>(A, B);
+  combine_from<kRowBcast15, 0xa>(A, B);  // lane 15 -> row 1, lane 47 -> row 3
+  combine_from<kRowBcast31, 0xc>(A, B);  // lane 31 -> rows 2 and 3
+}
+
+// Inclusive scan inside aligned segments of G lanes (G in {4, 8, 16, 32}); sl = lane % G.
+template <int G>
+__device__ __forceinline__ void segment_scan(float& A, float& B, int sl) {
+  if constexpr (G >= 16) {
+    combine_from<kRowShr1>(A, B);
+    combine_from<kRowShr2>(A, B);
+    combine_from<kRowShr4>(A, B);
+    combine_from<kRowShr8>(A, B);
+    if constexpr (G == 32) combine_from<kRowBcast15, 0xa>(A, B);
+  } else {
+    combine_from_masked<kRowShr1>(A, B, sl >= 1);
+    combine_from_masked<kRowShr2>(A, B, sl >= 2);
+    if constexpr (G == 8) combine_from_masked<kRowShr4>(A, B, sl >= 4);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Launch arguments. Modes: 0 forward, 1 reverse, 2 fused backward (a reverse scan).
+// fwd/rev: in0 = gates, in1 = tokens, out0 = out.
+// bwd:     in0 = gates, in1 = grad_out, in2 = saved forward output, out0 = grad_tokens,
+//          out1 = grad_gates.
+// ---------------------------------------------------------------------------------------
+struct Args {
+  const void* in0;
+  const void* in1;
+  const void* in2;
+  void* out0;
+  void* out1;
+  int64_t rows;
+  int64_t dim;
+  int64_t stride_b;
+  int64_t stride_d;
+  int32_t seqlen;
+  int32_t contiguous;
+};
+
+constexpr int kFwd = 0;
+constexpr int kRev = 1;
+constexpr int kBwd = 2;
+
+__device__ __forceinline__ int64_t row_offset(const Args& a, int64_t row) {
+  if (a.contiguous) return row * a.seqlen;
+  const int64_t b = row / a.dim;
+  const int64_t d = row - b * a.dim;
+  return b * a.stride_b + d * a.stride_d;
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* base, int64_t elem, int size) {
+  return *reinterpret_cast<const u32x4*>(static_cast<const char*>(base) + elem * size);
+}
+
+__device__ __forceinline__ void st16(void* base, int64_t elem, int size, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * size));
+}
+
+// Buffer resources: one per tensor per row, base = the row's first element, range = the
+// row's bytes. Loads and stores then carry only a 32-bit in-row byte offset in a VGPR, and
+// the hardware range check turns any offset outside the row into a zero read / dropped
+// write instead of a fault.
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+constexpr int kCacheNT = 2;             // cache-policy bit: nontemporal (streaming) store
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+__device__ __forceinline__ Rsrc row_rsrc(const void* p, int64_t row_base, int size, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(static_cast<const char*>(p)) + row_base * size, (short)0, bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4 bld16(Rsrc r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ void bst16(Rsrc r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCacheNT);
+}
+
+template <class E>
+__device__ __forceinline__ float bld1(Rsrc r, uint32_t off) {
+  if constexpr (E::kSize == 4) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  } else {
+    return E::widen16(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+  }
+}
+
+// Loaded operands of one sub-chunk for one lane, plus the two wave-uniform boundary values
+// the backward needs: the gate just past the sub-chunk and the output just before it.
+template <int kMode>
+struct Slot {
+  u32x4 v[kMode == kBwd ? 3 : 2];
+  float gate_after;
+  float out_before;
+};
+
+template <int kMode>
+struct RowRsrc {
+  Rsrc in0, in1, in2, out0, out1;
+};
+
+// Byte offset that no row range contains: loads from it return 0 without touching memory.
+constexpr uint32_t kNoOffset = 0x80000000u;
+
+// Issues the loads of one sub-chunk. `sub_bytes` is the wave-uniform byte offset of the
+// sub-chunk inside the row, or kNoOffset for a ring slot past the end of the row (the loads
+// are still issued so that the wait counts stay static). Boundary values read outside the
+// row come back as 0 and are replaced by the identity where they are used.
+template <class E, int kMode>
+__device__ __forceinline__ void load_slot(const RowRsrc<kMode>& rr, Slot<kMode>& s,
+                                          uint32_t sub_bytes, uint32_t lane_off) {
+  constexpr int kSubBytes = 64 * 16;
+  const uint32_t off = sub_bytes + lane_off;
+  s.v[0] = bld16(rr.in0, off);
+  s.v[1] = bld16(rr.in1, off);
+  if constexpr (kMode == kBwd) {
+    s.v[2] = bld16(rr.in2, off);
+    s.gate_after = bld1<E>(rr.in0, sub_bytes + kSubBytes);
+    s.out_before = bld1<E>(rr.in2, sub_bytes - E::kSize);
+  }
+}
+
+// Builds the per-lane affine maps (alpha, beta) in processing order from a loaded slot.
+// For the backward also returns y[t-1] per element (processing order) in ysh.
+// `gate_next`/`out_prev` are the neighbour values for the lanes at the edges of the span
+// (uniform boundary values for long rows, the identity for short-row segments);
+// `span_first_lane`/`span_last_lane` say whether this lane is the first/last lane of its
+// span in processing order.
+template <class E, int kMode>
+__device__ __forceinline__ void make_maps(const Slot<kMode>& s, float (&al)[E::V], float (&be)[E::V],
+                                          float (&ysh)[E::V], float gate_next, float out_prev,
+                                          bool span_first_lane, bool span_last_lane) {
+  constexpr int V = E::V;
+  float g[V], x[V];
+  E::unpack(s.v[0], g);
+  E::unpack(s.v[1], x);
+  if constexpr (kMode == kBwd) {
+    float y[V];
+    E::unpack(s.v[2], y);
+    // gates[t+1]: inside the vector, then from the lane holding the next vector in memory
+    // (scan lane - 1, wave_shr:1); the span's first lane (memory-last vector) takes gate_next.
+    float gs_last = dpp<kWaveShr1>(gate_next, g[0]);
+    gs_last = span_first_lane ? gate_next : gs_last;
+    // y[t-1]: inside the vector, then from the lane holding the previous vector in memory
+    // (scan lane + 1, wave_shl:1); the span's last lane (memory-first vector) takes out_prev.
+    float ys_first = dpp<kWaveShl1>(out_prev, y[V - 1]);
+    ys_first = span_last_lane ? out_prev : ys_first;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const int e = V - 1 - k;  // memory index, processed last-to-first
+      al[k] = (e == V - 1) ? gs_last : g[e + 1];
+      be[k] = x[e];
+      ysh[k] = (e == 0) ? ys_first : y[e - 1];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const int e = (kMode == kRev) ? V - 1 - k : k;
+      al[k] = g[e];
+      be[k] = x[e];
+      ysh[k] = 0.0f;
+    }
+  }
+}
+
+template <class E>
+__device__ __forceinline__ void lane_aggregate(const float (&al)[E::V], const float (&be)[E::V],
+                                               float& A, float& B) {
+  A = al[0];
+  B = be[0];
+#pragma unroll
+  for (int k = 1; k < E::V; ++k) {
+    B = fmaf(al[k], B, be[k]);
+    A = A * al[k];
+  }
+}
+
+// Re-runs the lane's elements from the value entering the lane; returns the packed output
+// vector(s) in memory order (o1 only for the backward: grad_gates).
+template <class E, int kMode>
+__device__ __forceinline__ void finish_lane(const float (&al)[E::V], const float (&be)[E::V],
+                                            const float (&ysh)[E::V], float y, u32x4& o0,
+                                            u32x4& o1) {
+  constexpr int V = E::V;
+  float res[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    y = fmaf(al[k], y, be[k]);
+    res[k] = y;
+  }
+  float om[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) om[e] = (kMode == kFwd) ? res[e] : res[V - 1 - e];
+  o0 = E::pack(om);
+  if constexpr (kMode == kBwd) {
+    float gg[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) gg[e] = om[e] * ysh[V - 1 - e];
+    o1 = E::pack(gg);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Long rows: W waves per row, U sub-chunks in flight per wave.
+// ---------------------------------------------------------------------------------------
+template <class E, int kMode, int W, int U>
+__global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Args a) {
+  constexpr int V = E::V;
+  constexpr int kSub = 64 * V;
+  constexpr bool kReverse = kMode != kFwd;
+  constexpr int kRowsPerBlock = (W == 1) ? 4 : 1;
+
+  __shared__ f32x2 exch[2][W];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = (W == 1) ? 0 : wave;
+  const int vec = kReverse ? 63 - lane : lane;  // memory vector of this lane in a sub-chunk
+  const uint32_t lane_off = (uint32_t)vec * 16u;
+  const int nsub = a.seqlen / kSub;
+  const int nrounds = nsub / W;
+  const int row_bytes = a.seqlen * E::kSize;
+  const int64_t ngroups = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+
+  for (int64_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+    const int64_t row = grp * kRowsPerBlock + ((W == 1) ? wave : 0);
+    if (W == 1 && row >= a.rows) break;  // wave-uniform; no barriers when W == 1
+    const int64_t base = row_offset(a, row);
+    RowRsrc<kMode> rr;
+    rr.in0 = row_rsrc(a.in0, base, E::kSize, row_bytes);
+    rr.in1 = row_rsrc(a.in1, base, E::kSize, row_bytes);
+    rr.out0 = row_rsrc(a.out0, base, E::kSize, row_bytes);
+    if constexpr (kMode == kBwd) {
+      rr.in2 = row_rsrc(a.in2, base, E::kSize, row_bytes);
+      rr.out1 = row_rsrc(a.out1, base, E::kSize, row_bytes);
+    }
+
+    // byte offset inside the row of the sub-chunk this wave handles in round r
+    auto sub_bytes = [&](int r) -> uint32_t {
+      const int j = r * W + w;
+      return (uint32_t)((kReverse ? (nsub - 1 - j) : j) * kSub * E::kSize);
+    };
+
+    Slot<kMode> ring[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      load_slot<E, kMode>(rr, ring[u], sub_bytes(u), lane_off);
+      __builtin_amdgcn_sched_barrier(0);  // slot u's loads before slot u+1's (wait counts)
+    }
+
+    float carry = 0.0f;
+    for (int r0 = 0; r0 < nrounds; r0 += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = r0 + u;
+        const uint32_t sb = sub_bytes(r);
+        float gate_next = 1.0f, out_prev = 0.0f;
+        if constexpr (kMode == kBwd) {
+          // identity at the row edges: gates[L] = 1, y[-1] = 0
+          gate_next = (sb + kSub * E::kSize < (uint32_t)row_bytes) ? ring[u].gate_after : 1.0f;
+          out_prev = (sb > 0) ? ring[u].out_before : 0.0f;
+        }
+        float al[V], be[V], ysh[V];
+        make_maps<E, kMode>(ring[u], al, be, ysh, gate_next, out_prev, lane == 0, lane == 63);
+        if (kMode != kBwd && r == 0 && w == 0 && lane == 0) {
+          // the first element of the row in processing order never uses its gate
+          // (gates[0] forward, gates[L-1] reverse), as in full_scan.cu:96
+          al[0] = 1.0f;
+        }
+        float A, B;
+        lane_aggregate<E>(al, be, A, B);
+        wave_scan(A, B);
+        float c_in = carry;
+        if constexpr (W == 1) {
+          carry = fmaf(readlane(A, 63), carry, readlane(B, 63));
+        } else {
+          // the W sub-chunk aggregates of this round, scanned across lanes 0..W-1 (one DPP row)
+          if (lane == 63) exch[r & 1][w] = f32x2{A, B};
+          __syncthreads();
+          float eA = 1.0f, eB = 0.0f;
+          if (lane < W) {
+            const f32x2 t = exch[r & 1][lane];
+            eA = t.x;
+            eB = t.y;
+          }
+          combine_from<kRowShr1>(eA, eB);
+          if constexpr (W > 2) combine_from<kRowShr2>(eA, eB);
+          if constexpr (W > 4) combine_from<kRowShr4>(eA, eB);
+          if constexpr (W > 8) combine_from<kRowShr8>(eA, eB);
+          if (w > 0) c_in = fmaf(readlane(eA, w - 1), carry, readlane(eB, w - 1));
+          carry = fmaf(readlane(eA, W - 1), carry, readlane(eB, W - 1));
+        }
+        const float y_lane_end = fmaf(A, c_in, B);
+        const float y_enter = dpp<kWaveShr1>(c_in, y_lane_end);
+        u32x4 o0, o1;
+        finish_lane<E, kMode>(al, be, ysh, y_enter, o0, o1);
+        bst16(rr.out0, sb + lane_off, o0);
+        if constexpr (kMode == kBwd) bst16(rr.out1, sb + lane_off, o1);
+        const uint32_t next = (r + U < nrounds) ? sub_bytes(r + U) : kNoOffset;
+        load_slot<E, kMode>(rr, ring[u], next, lane_off);
+        // keep the ring order: without this the scheduler hoists the next slot's arithmetic
+        // above this slot's refill, which turns every wait into a wait for all loads
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Short rows: G lanes per row (seqlen = G * V), 64/G rows per wave, 4 waves per block.
+// ---------------------------------------------------------------------------------------
+template <class E, int kMode, int G>
+__global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
+  constexpr int V = E::V;
+  constexpr bool kReverse = kMode != kFwd;
+  constexpr int kRowsPerWave = 64 / G;
+  constexpr int kRowsPerBlock = 4 * kRowsPerWave;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sl = lane & (G - 1);
+  const int seg = lane / G;
+  const int vec = kReverse ? G - 1 - sl : sl;
+  const int64_t ngroups = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+
+  for (int64_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+    const int64_t wave_row0 = grp * kRowsPerBlock + (int64_t)wave * kRowsPerWave;
+    if (wave_row0 >= a.rows) break;  // wave-uniform
+    const int64_t row = wave_row0 + seg;
+    const bool valid = row < a.rows;
+    const int64_t base = valid ? row_offset(a, row) : 0;
+
+    Slot<kMode> s;
+    if (valid) {
+      const int64_t e = base + (int64_t)vec * V;
+      s.v[0] = ld16(a.in0, e, E::kSize);
+      s.v[1] = ld16(a.in1, e, E::kSize);
+      if constexpr (kMode == kBwd) s.v[2] = ld16(a.in2, e, E::kSize);
+    } else {
+#pragma unroll
+      for (int i = 0; i < (kMode == kBwd ? 3 : 2); ++i) s.v[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+    float al[V], be[V], ysh[V];
+    make_maps<E, kMode>(s, al, be, ysh, 1.0f, 0.0f, sl == 0, sl == G - 1);
+    if (kMode != kBwd && sl == 0) al[0] = 1.0f;
+    float A, B;
+    lane_aggregate<E>(al, be, A, B);
+    segment_scan<G>(A, B, sl);
+    float y_enter = dpp<kWaveShr1>(0.0f, B);
+    y_enter = (sl == 0) ? 0.0f : y_enter;
+    u32x4 o0, o1;
+    finish_lane<E, kMode>(al, be, ysh, y_enter, o0, o1);
+    if (valid) {
+      st16(a.out0, base + (int64_t)vec * V, E::kSize, o0);
+      if constexpr (kMode == kBwd) st16(a.out1, base + (int64_t)vec * V, E::kSize, o1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------------
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+std::atomic<int> g_override_w{0};
+std::atomic<int> g_override_u{0};
+
+int cu_count(int* status) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    *status = FPSCAN_ERR_DEVICE;
+    return 0;
+  }
+  if (dev < kMaxDevices) {
+    const int cached = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0) {
+    *status = FPSCAN_ERR_DEVICE;
+    return 0;
+  }
+  if (dev < kMaxDevices) g_cu_count[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+int launch(const void* kernel, int64_t groups, int threads, const Args& a, hipStream_t stream) {
+  // One group per block; very large problems loop inside the kernel (grid-stride) so the
+  // dispatch stays below 2^31 work-items.
+  const int64_t max_blocks = ((int64_t)1 << 31) / threads;
+  const unsigned int blocks = (unsigned int)(groups < max_blocks ? groups : max_blocks);
+  Args copy = a;
+  void* params[] = {&copy};
+  const hipError_t err =
+      hipLaunchKernel(kernel, dim3(blocks), dim3(threads), params, 0, stream);
+  return err == hipSuccess ? FPSCAN_OK : FPSCAN_ERR_LAUNCH;
+}
+
+template <class E, int kMode, int W>
+const void* long_kernel(int u) {
+  if constexpr (W == 1) {
+    if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4>);
+  }
+  // W > 1 keeps at most two sub-chunks in flight per wave: the W waves of a row already
+  // multiply the bytes in flight, and deeper rings exceed 64 VGPRs.
+  if (u >= 2) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 2>);
+  return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 1>);
+}
+
+template <class E, int kMode>
+const void* long_kernel(int w, int u) {
+  switch (w) {
+    case 1: return long_kernel<E, kMode, 1>(u);
+    case 2: return long_kernel<E, kMode, 2>(u);
+    case 4: return long_kernel<E, kMode, 4>(u);
+    case 8: return long_kernel<E, kMode, 8>(u);
+    default: return long_kernel<E, kMode, 16>(u);
+  }
+}
+
+template <class E, int kMode>
+const void* short_kernel(int g) {
+  switch (g) {
+    case 4: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 4>);
+    case 8: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 8>);
+    case 16: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 16>);
+    default: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 32>);
+  }
+}
+
+// Chooses the launch for one problem. Rows are independent; a row is owned by W waves so
+// that rows * W reaches one full occupancy round of the device (32 waves per CU).
+template <class E, int kMode>
+int run(const Args& a, hipStream_t stream) {
+  constexpr int V = E::V;
+  constexpr int kSub = 64 * V;
+  const int L = a.seqlen;
+  if (L < kSub) {
+    const int g = L / V;
+    const int64_t rows_per_block = 4 * (64 / g);
+    return launch(short_kernel<E, kMode>(g), (a.rows + rows_per_block - 1) / rows_per_block,
+                  256, a, stream);
+  }
+  int status = FPSCAN_OK;
+  const int cus = cu_count(&status);
+  if (status != FPSCAN_OK) return status;
+  const int nsub = L / kSub;
+  const int64_t target_waves = (int64_t)cus * 32;
+  int w = 1;
+  while (w < 16 && 2 * w <= nsub && a.rows * w < target_waves) w *= 2;
+  int u_max = (kMode == kBwd) ? E::kRingBwd : E::kRingFwd;
+  if (w > 1 && u_max > 2) u_max = 2;
+  const int ow = g_override_w.load(std::memory_order_relaxed);
+  const int ou = g_override_u.load(std::memory_order_relaxed);
+  if (ow > 0) w = ow <= nsub ? ow : nsub;
+  if (ou > 0) u_max = ou;
+  const int nrounds = nsub / w;
+  const int u = u_max < nrounds ? u_max : nrounds;
+  if (w == 1) return launch(long_kernel<E, kMode>(1, u), (a.rows + 3) / 4, 256, a, stream);
+  return launch(long_kernel<E, kMode>(w, u), a.rows, 64 * w, a, stream);
+}
+
+template <int kMode>
+int dispatch(int dtype, const Args& a, hipStream_t stream) {
+  switch (dtype) {
+    case FPSCAN_DTYPE_F32: return run<F32, kMode>(a, stream);
+    case FPSCAN_DTYPE_F16: return run<F16, kMode>(a, stream);
+    case FPSCAN_DTYPE_BF16: return run<BF16, kMode>(a, stream);
+    default: return FPSCAN_ERR_DTYPE;
+  }
+}
+
+int itemsize(int dtype) {
+  switch (dtype) {
+    case FPSCAN_DTYPE_F32: return 4;
+    case FPSCAN_DTYPE_F16: return 2;
+    case FPSCAN_DTYPE_BF16: return 2;
+    default: return 0;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shared argument validation. Mirrors the reference's checks where it has them
+// (seqlen table full_scan.cu:207-233, dtype full_scan.cu:245-256) and adds the ones it
+// lacks (shape, alignment, null pointers).
+int validate(int64_t batch, int64_t dim, int64_t seqlen, int64_t stride_b, int64_t stride_d,
+             int dtype, Args* a) {
+  if (seqlen < 32 || seqlen > 65536 || (seqlen & (seqlen - 1)) != 0) return FPSCAN_ERR_SEQLEN;
+  const int size = itemsize(dtype);
+  if (size == 0) return FPSCAN_ERR_DTYPE;
+  if (batch < 0 || dim < 0 || stride_b < 0 || stride_d < 0) return FPSCAN_ERR_SHAPE;
+  if (dim > 1 && stride_d < seqlen) return FPSCAN_ERR_SHAPE;
+  if (batch > 1 && dim > 0 && stride_b < (dim - 1) * stride_d + seqlen) return FPSCAN_ERR_SHAPE;
+  // strides of size-1 dimensions are never used
+  if (batch > 1 && ((stride_b * size) & 15) != 0) return FPSCAN_ERR_ALIGN;
+  if (dim > 1 && ((stride_d * size) & 15) != 0) return FPSCAN_ERR_ALIGN;
+  a->rows = batch * dim;
+  a->dim = dim > 0 ? dim : 1;
+  a->stride_b = stride_b;
+  a->stride_d = stride_d;
+  a->seqlen = (int32_t)seqlen;
+  // row r starts at r * seqlen exactly when both strides are the packed ones
+  a->contiguous = (dim <= 1 || stride_d == seqlen) && (batch <= 1 || stride_b == dim * seqlen);
+  return FPSCAN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fpscan_scan_fwd(const void* gates, const void* tokens, void* out, int64_t batch, int64_t dim,
+                    int64_t seqlen, int64_t stride_b, int64_t stride_d, int dtype, int reverse,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  Args a{};
+  const int st = validate(batch, dim, seqlen, stride_b, stride_d, dtype, &a);
+  if (st != FPSCAN_OK) return st;
+  if (a.rows == 0) return FPSCAN_OK;
+  if (!gates || !tokens || !out) return FPSCAN_ERR_NULL;
+  if (!aligned16(gates) || !aligned16(tokens) || !aligned16(out)) return FPSCAN_ERR_ALIGN;
+  a.in0 = gates;
+  a.in1 = tokens;
+  a.out0 = out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return reverse ? dispatch<kRev>(dtype, a, s) : dispatch<kFwd>(dtype, a, s);
+}
+
+int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out, void* grad_gates,
+                    void* grad_tokens, int64_t batch, int64_t dim, int64_t seqlen,
+                    int64_t stride_b, int64_t stride_d, int dtype, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  Args a{};
+  const int st = validate(batch, dim, seqlen, stride_b, stride_d, dtype, &a);
+  if (st != FPSCAN_OK) return st;
+  if (a.rows == 0) return FPSCAN_OK;
+  if (!gates || !out || !grad_out || !grad_gates || !grad_tokens) return FPSCAN_ERR_NULL;
+  if (!aligned16(gates) || !aligned16(out) || !aligned16(grad_out) || !aligned16(grad_gates) ||
+      !aligned16(grad_tokens))
+    return FPSCAN_ERR_ALIGN;
+  a.in0 = gates;
+  a.in1 = grad_out;
+  a.in2 = out;
+  a.out0 = grad_tokens;
+  a.out1 = grad_gates;
+  return dispatch<kBwd>(dtype, a, static_cast<hipStream_t>(stream));
+}
+
+size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype, int op) {
+  (void)batch;
+  (void)dim;
+  (void)seqlen;
+  (void)dtype;
+  (void)op;
+  return 0;
+}
+
+const char* fpscan_strerror(int status) {
+  switch (status) {
+    case FPSCAN_OK: return "success";
+    case FPSCAN_ERR_SEQLEN: return "seqlen must be a power of 2, >= 32, <= 65536";
+    case FPSCAN_ERR_DTYPE: return "Unsupported tensor dtype: expecting bfloat16, float16 or float32";
+    case FPSCAN_ERR_SHAPE: return "invalid shape or strides: rows must not overlap";
+    case FPSCAN_ERR_ALIGN: return "data pointers and row strides must be 16-byte aligned";
+    case FPSCAN_ERR_NULL: return "null data pointer";
+    case FPSCAN_ERR_WORKSPACE: return "workspace too small";
+    case FPSCAN_ERR_LAUNCH: return "HIP kernel launch failed";
+    case FPSCAN_ERR_DEVICE: return "could not query the current HIP device";
+    default: return "unknown fpscan status";
+  }
+}
+
+int fpscan_abi_version(void) { return FPSCAN_ABI_VERSION; }
+
+int fpscan_set_launch_override(int waves_per_row, int ring_depth) {
+  const bool w_ok = waves_per_row == 0 || waves_per_row == 1 || waves_per_row == 2 ||
+                    waves_per_row == 4 || waves_per_row == 8 || waves_per_row == 16;
+  const bool u_ok = ring_depth == 0 || ring_depth == 1 || ring_depth == 2 || ring_depth == 4;
+  if (!w_ok || !u_ok) return FPSCAN_ERR_SHAPE;
+  g_override_w.store(waves_per_row, std::memory_order_relaxed);
+  g_override_u.store(ring_depth, std::memory_order_relaxed);
+  return FPSCAN_OK;
+}
+
+}  // extern "C"

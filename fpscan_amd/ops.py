@@ -1,0 +1,112 @@
+"""Python API of the MI355X scan: ``scan_forward``, ``PScan`` and ``pscan``.
+
+Drop-in for ``fpscan/ops.py`` of saeeddhqan/fpscan:
+
+* ``_load_extension`` mirrors fpscan/ops.py:20-44 (first importable candidate that exposes
+  ``fullscan_forward``, ImportError listing every failure otherwise). There is no fallback:
+  without the built HIP extension every entry point raises.
+* ``scan_forward`` mirrors fpscan/ops.py:47-58 (caller-provided or freshly allocated ``out``,
+  returned after the call).
+* ``PScan.forward`` mirrors fpscan/ops.py:63-67 (saves ``(gates, out)``).
+* ``PScan.backward`` replaces fpscan/ops.py:69-83 (shifted-gate copy, reverse scan,
+  shifted-output copy, product: 7 ATen launches and one scan) with one fused HIP kernel that
+  reads gates, out and grad_out once and writes both gradients.
+* ``pscan`` mirrors fpscan/ops.py:86-87.
+"""
+from __future__ import annotations
+
+import importlib
+from typing import Optional, Tuple
+
+import torch
+
+__all__ = ["pscan", "scan_forward", "scan_backward", "PScan"]
+
+_EXT_CANDIDATES = ("fpscan_amd._C",)
+_ext = None
+
+
+def _load_extension():
+    global _ext
+    if _ext is not None:
+        return _ext
+
+    errors = []
+    for name in _EXT_CANDIDATES:
+        try:
+            module = importlib.import_module(name)
+        except Exception as exc:  # not built / wrong arch / missing ROCm runtime
+            errors.append(f"  {name}: {exc}")
+            continue
+        if hasattr(module, "fullscan_forward"):
+            _ext = module
+            return _ext
+        errors.append(f"  {name}: imported but has no 'fullscan_forward'")
+
+    raise ImportError(
+        "Could not import the fpscan HIP extension. Build it first "
+        "(`python -c 'import __graft_entry__ as g; g.build()'` from the repository root, "
+        "or `python -m fpscan_amd._build`). Tried:\n" + "\n".join(errors)
+    )
+
+
+def scan_forward(
+    gates: torch.Tensor,
+    tokens: torch.Tensor,
+    reverse: bool = False,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """y[t] = gates[t]*y[t-1] + tokens[t] along the last axis (reverse: y[t+1]), y = 0 before
+    the first element. (batch, dim, seqlen) contiguous fp32/fp16/bf16 on the GPU, seqlen a
+    power of two in [32, 65536]; fp32 accumulation. Writes into ``out`` when given."""
+    ext = _load_extension()
+    if out is None:
+        out = torch.empty_like(tokens)
+    ext.fullscan_forward(gates, tokens, out, reverse)
+    return out
+
+
+def scan_backward(
+    gates: torch.Tensor,
+    out: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_gates: Optional[torch.Tensor] = None,
+    grad_tokens: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gradients of the forward scan given its output ``out``:
+    grad_tokens[t] = grad_out[t] + gates[t+1]*grad_tokens[t+1] (gates[L] = 1) and
+    grad_gates[t] = grad_tokens[t]*out[t-1] (out[-1] = 0). Returns (grad_gates, grad_tokens).
+    """
+    ext = _load_extension()
+    if grad_gates is None:
+        grad_gates = torch.empty_like(gates)
+    if grad_tokens is None:
+        grad_tokens = torch.empty_like(gates)
+    ext.fullscan_backward(gates, out, grad_out, grad_gates, grad_tokens)
+    return grad_gates, grad_tokens
+
+
+class PScan(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+        out = scan_forward(gates, tokens)
+        ctx.save_for_backward(gates, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        gates, out = ctx.saved_tensors
+        grad_output = grad_output.contiguous()
+        grad_gates, grad_tokens = scan_backward(gates, out, grad_output)
+        return grad_gates, grad_tokens
+
+
+def pscan(gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    return PScan.apply(gates, tokens)
+
+
+def set_launch_override(waves_per_row: int = 0, ring_depth: int = 0) -> None:
+    """Tuning hook: force the number of waves per row and the per-wave ring depth of the
+    long-row kernels (0 restores the built-in choice). Process-wide."""
+    _load_extension().set_launch_override(int(waves_per_row), int(ring_depth))

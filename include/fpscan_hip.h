@@ -1,0 +1,107 @@
+/*
+ * fpscan_hip.h -- C ABI of the MI355X (gfx950) first-order linear-recurrence scan.
+ *
+ *   forward:  y[t] = gates[t] * y[t-1] + tokens[t],   y[-1] = 0
+ *   reverse:  y[t] = gates[t] * y[t+1] + tokens[t],   y[L]  = 0
+ *   backward: grad_tokens[t] = grad_out[t] + gates[t+1] * grad_tokens[t+1]  (gates[L] = 1)
+ *             grad_gates[t]  = grad_tokens[t] * y[t-1]                     (y[-1]   = 0)
+ *
+ * Tensors are (batch, dim, seqlen) with the seqlen axis contiguous; row (b, d) starts at
+ * element offset b*stride_b + d*stride_d. Every tensor passed to one call shares that layout.
+ * Element types: fp32, fp16 and bf16; all arithmetic is fp32, outputs are rounded to
+ * nearest-even once. seqlen must be a power of two in [32, 65536], as in the reference.
+ *
+ * All entry points are asynchronous on `stream` (a hipStream_t; NULL = the null stream),
+ * allocate nothing, keep no state between calls and are safe to call from several host
+ * threads. Pointers are device pointers on the current HIP device; they must be 16-byte
+ * aligned and the strides must be multiples of 16 bytes (16/itemsize elements).
+ *
+ * Reference interface replaced (saeeddhqan/fpscan):
+ *   csrc/main.cpp:7-11              PYBIND11_MODULE: "fullscan_forward" -> warpscan_fwd
+ *   csrc/full_scan/full_scan.h:26-36 warpscan_fwd(Ax, Bx, out, reverse)
+ *   csrc/full_scan/full_scan.cu:179-258 warpscan<T> / warpscan_forward (dtype dispatch,
+ *                                    tile table, launch on the current stream)
+ *   fpscan/ops.py:69-83             PScan.backward (7 ATen ops + a reverse scan), fused here
+ */
+#ifndef FPSCAN_HIP_H
+#define FPSCAN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FPSCAN_ABI_VERSION 1
+
+/* Element type codes (the reference dispatches on the same three types,
+ * full_scan.cu:245-256). */
+#define FPSCAN_DTYPE_F32 0
+#define FPSCAN_DTYPE_F16 1
+#define FPSCAN_DTYPE_BF16 2
+
+/* Operation codes for fpscan_workspace_bytes. */
+#define FPSCAN_OP_FWD 0
+#define FPSCAN_OP_BWD 1
+
+/* Status codes. The reference raises RuntimeError through TORCH_CHECK for the first
+ * three conditions (full_scan.cu:181-182, 232, 240-256); the binding maps every nonzero
+ * status to RuntimeError with fpscan_strerror's text. */
+#define FPSCAN_OK 0
+#define FPSCAN_ERR_SEQLEN 1    /* seqlen not a power of two in [32, 65536] */
+#define FPSCAN_ERR_DTYPE 2     /* dtype code not one of FPSCAN_DTYPE_* */
+#define FPSCAN_ERR_SHAPE 3     /* negative batch/dim/stride or rows that overlap */
+#define FPSCAN_ERR_ALIGN 4     /* pointer or stride not 16-byte aligned */
+#define FPSCAN_ERR_NULL 5      /* null data pointer with a non-empty problem */
+#define FPSCAN_ERR_WORKSPACE 6 /* workspace smaller than fpscan_workspace_bytes() */
+#define FPSCAN_ERR_LAUNCH 7    /* hipGetLastError() reported a failure after the launch */
+#define FPSCAN_ERR_DEVICE 8    /* the current device could not be queried */
+
+/* Forward or reverse scan.
+ * Replaces warpscan_fwd / warpscan_forward (csrc/full_scan/full_scan.h:26-36,
+ * csrc/full_scan/full_scan.cu:238-258); `gates`/`tokens` are the reference's Ax/Bx and
+ * `out` is written in full (the reference's caller allocates it, fpscan/ops.py:55-56).
+ * `out` may alias `tokens` or `gates` exactly (in-place scan). */
+int fpscan_scan_fwd(const void* gates, const void* tokens, void* out,
+                    int64_t batch, int64_t dim, int64_t seqlen,
+                    int64_t stride_b, int64_t stride_d,
+                    int dtype, int reverse,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused backward of the forward scan, given the saved forward output `out`.
+ * Replaces the composition in PScan.backward (fpscan/ops.py:69-83): shifted-gate copy,
+ * reverse scan (full_scan.cu:198-200), shifted-output copy and the product, in one pass
+ * that reads gates, out and grad_out and writes grad_gates and grad_tokens. */
+int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out,
+                    void* grad_gates, void* grad_tokens,
+                    int64_t batch, int64_t dim, int64_t seqlen,
+                    int64_t stride_b, int64_t stride_d,
+                    int dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device workspace, in bytes, that fpscan_scan_fwd/fpscan_scan_bwd need for this problem
+ * (0 when none). No reference counterpart: the reference kernel keeps its carries in
+ * shared memory (full_scan.cu:55-57). */
+size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype, int op);
+
+/* Static description of a status code (never NULL). The reference's equivalent is the
+ * TORCH_CHECK message text (full_scan.h:7-9). */
+const char* fpscan_strerror(int status);
+
+/* FPSCAN_ABI_VERSION of the loaded library. */
+int fpscan_abi_version(void);
+
+/* Launch-shape override for tuning sweeps; process-wide, not synchronised with calls in
+ * flight on other threads. waves_per_row in {0,1,2,4,8,16}, ring_depth in {0,1,2,4};
+ * 0 restores the built-in choice. Every setting computes the same recurrence; only the
+ * grouping of fp32 partial products (and so the last-bit rounding) changes. The ring
+ * depth never changes results. No reference counterpart: the
+ * reference fixes its tiles at compile time (full_scan.cu:207-233). */
+int fpscan_set_launch_override(int waves_per_row, int ring_depth);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FPSCAN_HIP_H */

@@ -1,0 +1,175 @@
+"""CPU checks of the drop-in boundary: the C-ABI library and the torch binding load, export
+what include/fpscan_hip.h declares, and reject bad arguments before any HIP call.
+
+No kernel is launched here (no GPU in this container): every call below fails validation
+first, which the C ABI does before touching the HIP runtime.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "fpscan_hip.h")
+LIB = os.path.join(ROOT, "fpscan_amd", "libfpscan_hip.so")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(fpscan_\w+)\s*\(", text, flags=re.M)
+
+
+def header_defines():
+    text = open(HEADER).read()
+    return {m.group(1): int(m.group(2)) for m in
+            re.finditer(r"#define\s+(FPSCAN_\w+)\s+(\d+)", text)}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built; run __graft_entry__.build() first")
+    lib = ctypes.CDLL(LIB)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_scan_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                    ctypes.c_int, vp, ctypes.c_size_t, vp]
+    lib.fpscan_scan_fwd.restype = ctypes.c_int
+    lib.fpscan_scan_bwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                    vp, ctypes.c_size_t, vp]
+    lib.fpscan_scan_bwd.restype = ctypes.c_int
+    lib.fpscan_strerror.argtypes = [ctypes.c_int]
+    lib.fpscan_strerror.restype = ctypes.c_char_p
+    lib.fpscan_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int, ctypes.c_int]
+    lib.fpscan_workspace_bytes.restype = ctypes.c_size_t
+    lib.fpscan_set_launch_override.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.fpscan_set_launch_override.restype = ctypes.c_int
+    return lib
+
+
+def test_header_declares_the_expected_entry_points():
+    names = header_functions()
+    assert {"fpscan_scan_fwd", "fpscan_scan_bwd", "fpscan_workspace_bytes", "fpscan_strerror",
+            "fpscan_abi_version", "fpscan_set_launch_override"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} declared in fpscan_hip.h but not exported"
+
+
+def test_abi_version_matches_header(lib):
+    assert lib.fpscan_abi_version() == header_defines()["FPSCAN_ABI_VERSION"]
+
+
+def test_strerror_covers_every_status(lib):
+    d = header_defines()
+    codes = [v for k, v in d.items() if k == "FPSCAN_OK" or k.startswith("FPSCAN_ERR_")]
+    texts = {lib.fpscan_strerror(c).decode() for c in codes}
+    assert len(texts) == len(codes)  # one distinct message per status
+    assert lib.fpscan_strerror(999).decode() == "unknown fpscan status"
+    assert "power of 2" in lib.fpscan_strerror(d["FPSCAN_ERR_SEQLEN"]).decode()
+
+
+def test_workspace_is_zero(lib):
+    # the row-streaming kernels keep every carry in registers / LDS
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) == 0
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 1) == 0
+
+
+FAKE = 0x10000  # 16-byte aligned, never dereferenced: every call below fails validation
+
+
+@pytest.mark.parametrize("seqlen", [0, 16, 30, 48, 100, 131072])
+def test_bad_seqlen_rejected(lib, seqlen):
+    d = header_defines()
+    assert lib.fpscan_scan_fwd(FAKE, FAKE, FAKE, 2, 4, seqlen, 4 * seqlen, seqlen, 0, 0,
+                               None, 0, None) == d["FPSCAN_ERR_SEQLEN"]
+    assert lib.fpscan_scan_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, seqlen, 4 * seqlen, seqlen,
+                               0, None, 0, None) == d["FPSCAN_ERR_SEQLEN"]
+
+
+def test_bad_dtype_rejected(lib):
+    assert lib.fpscan_scan_fwd(FAKE, FAKE, FAKE, 2, 4, 64, 256, 64, 3, 0, None, 0, None) == \
+        header_defines()["FPSCAN_ERR_DTYPE"]
+
+
+def test_bad_shape_rejected(lib):
+    d = header_defines()
+    assert lib.fpscan_scan_fwd(FAKE, FAKE, FAKE, -1, 4, 64, 256, 64, 0, 0, None, 0, None) == \
+        d["FPSCAN_ERR_SHAPE"]
+    # rows overlapping: stride_d smaller than seqlen
+    assert lib.fpscan_scan_fwd(FAKE, FAKE, FAKE, 1, 4, 64, 256, 32, 0, 0, None, 0, None) == \
+        d["FPSCAN_ERR_SHAPE"]
+
+
+def test_misaligned_rejected(lib):
+    d = header_defines()
+    assert lib.fpscan_scan_fwd(FAKE + 4, FAKE, FAKE, 2, 4, 64, 256, 64, 0, 0, None, 0, None) \
+        == d["FPSCAN_ERR_ALIGN"]
+    # fp16 row stride of 36 elements = 72 bytes is not a multiple of 16
+    assert lib.fpscan_scan_fwd(FAKE, FAKE, FAKE, 1, 4, 32, 144, 36, 1, 0, None, 0, None) == \
+        d["FPSCAN_ERR_ALIGN"]
+
+
+def test_null_pointer_rejected_and_empty_problem_accepted(lib):
+    d = header_defines()
+    assert lib.fpscan_scan_fwd(None, FAKE, FAKE, 2, 4, 64, 256, 64, 0, 0, None, 0, None) == \
+        d["FPSCAN_ERR_NULL"]
+    # zero rows: nothing to do, no pointer is needed and nothing is launched
+    assert lib.fpscan_scan_fwd(None, None, None, 0, 4, 64, 256, 64, 0, 0, None, 0, None) == 0
+    assert lib.fpscan_scan_bwd(None, None, None, None, None, 2, 0, 64, 0, 64, 2, None, 0,
+                               None) == 0
+
+
+def test_launch_override_validation(lib):
+    d = header_defines()
+    assert lib.fpscan_set_launch_override(3, 0) == d["FPSCAN_ERR_SHAPE"]
+    assert lib.fpscan_set_launch_override(0, 3) == d["FPSCAN_ERR_SHAPE"]
+    assert lib.fpscan_set_launch_override(4, 2) == 0
+    assert lib.fpscan_set_launch_override(0, 0) == 0
+
+
+# ---------------------------------------------------------------- torch binding
+def test_binding_loads_and_exposes_the_reference_surface():
+    from fpscan_amd import ops
+
+    ext = ops._load_extension()
+    assert ext.__file__.startswith(os.path.join(ROOT, "fpscan_amd"))
+    for name in ("fullscan_forward", "fullscan_backward", "set_launch_override"):
+        assert hasattr(ext, name)
+
+
+def test_public_api_names():
+    import fpscan_amd
+
+    assert set(fpscan_amd.__all__) >= {"pscan", "scan_forward", "PScan"}
+
+
+@pytest.mark.parametrize("call", ["forward", "reverse", "pscan", "backward"])
+def test_cpu_tensors_raise_runtime_error(call):
+    import fpscan_amd
+
+    g, x = torch.rand(2, 4, 64), torch.rand(2, 4, 64)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        if call == "forward":
+            fpscan_amd.scan_forward(g, x)
+        elif call == "reverse":
+            fpscan_amd.scan_forward(g, x, reverse=True)
+        elif call == "pscan":
+            fpscan_amd.pscan(g, x)
+        else:
+            fpscan_amd.scan_backward(g, x, x)
+
+
+def test_missing_extension_raises_import_error(monkeypatch):
+    """fpscan/ops.py:40-44: no importable candidate -> ImportError naming each failure."""
+    from fpscan_amd import ops
+
+    monkeypatch.setattr(ops, "_ext", None)
+    monkeypatch.setattr(ops, "_EXT_CANDIDATES", ("fpscan_amd._no_such_module",))
+    with pytest.raises(ImportError, match="_no_such_module"):
+        ops.scan_forward(torch.rand(1, 1, 32), torch.rand(1, 1, 32))

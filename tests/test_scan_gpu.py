@@ -1,0 +1,404 @@
+"""GPU parity tests of the HIP scan against the CPU oracle (oracle/, pinned by
+tests/test_oracle.py).
+
+Mirrors the reference's tests/test_fpscan.py (forward at every seqlen, reverse, agreement with
+the Hillis-Steele baseline, backward through autograd, the two validation errors) with its
+tolerances (test_fpscan.py:18-22), and adds:
+
+* the north-star bar, normwise max|y - y*| / max|y*| against the float64 oracle on the same
+  rounded inputs: fp32 <= 1e-5, fp16 <= 5e-3, bf16 <= 2e-2 (outputs and both gradients);
+* fp16/bf16 at every seqlen, reverse and backward in every dtype (unpinned in the reference);
+* bit-exact known answers (tests/golden) and bit-exact size-independent properties at full
+  size: reverse == flip(forward(flip)), scaling tokens by 2 scales outputs by exactly 2, the
+  fused backward equals a reverse scan of the shifted gates;
+* every configuration of BASELINE.json at its real shape, and the edge cases the reference
+  does not test (ragged row counts, empty tensors, dim > 65535, `out=` and in-place use,
+  first-gate NaN, side streams, every launch shape).
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import fpscan_amd
+import oracle
+from fpscan_amd import ops
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a HIP device (MI355X)"),
+]
+
+DEVICE = "cuda"
+ALL_SEQLENS = [32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384, 32768, 65536]
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+REF_TOL = {  # reference tests/test_fpscan.py:18-22 (elementwise assert_close)
+    torch.float32: dict(atol=2e-3, rtol=2e-3),
+    torch.float16: dict(atol=3e-2, rtol=3e-2),
+    torch.bfloat16: dict(atol=6e-2, rtol=6e-2),
+}
+NORM_TOL = {torch.float32: 1e-5, torch.float16: 5e-3, torch.bfloat16: 2e-2}  # north star
+
+
+def make_inputs(batch, dim, seqlen, dtype, seed=0):
+    """test_fpscan.py:25-29 distributions, drawn on a seeded CPU generator (portable)."""
+    gen = torch.Generator().manual_seed(seed)
+    gates = 0.99 + 0.01 * torch.rand(batch, dim, seqlen, generator=gen)
+    tokens = torch.randn(batch, dim, seqlen, generator=gen) / seqlen
+    return gates.to(dtype).contiguous(), tokens.to(dtype).contiguous()
+
+
+def check(got, ref, dtype, what=""):
+    err = oracle.normwise_error(got, ref)
+    assert err <= NORM_TOL[dtype], f"{what}: normwise error {err:.3e} > {NORM_TOL[dtype]}"
+    torch.testing.assert_close(got.detach().double().cpu(), torch.from_numpy(np.asarray(ref)),
+                               **REF_TOL[dtype], msg=lambda m: f"{what}: {m}")
+    return err
+
+
+def bits_equal(a, b):
+    return torch.equal(a.contiguous().view(torch.int16 if a.element_size() == 2 else torch.int32),
+                       b.contiguous().view(torch.int16 if b.element_size() == 2 else torch.int32))
+
+
+# ------------------------------------------------------------------ reference test suite
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("seqlen", ALL_SEQLENS)
+def test_forward_matches_oracle(dtype, seqlen):
+    g, x = make_inputs(2, 4, seqlen, dtype, seed=seqlen)
+    out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE))
+    assert out.shape == x.shape and out.dtype == dtype and out.is_cuda
+    check(out, oracle.scan_f64(g, x), dtype, f"fwd {dtype} L{seqlen}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("seqlen", ALL_SEQLENS)
+def test_reverse_matches_oracle(dtype, seqlen):
+    g, x = make_inputs(2, 4, seqlen, dtype, seed=seqlen + 1)
+    out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE), reverse=True)
+    check(out, oracle.scan_f64(g, x, reverse=True), dtype, f"rev {dtype} L{seqlen}")
+
+
+@pytest.mark.parametrize("seqlen", [32, 256, 1024, 4096])
+def test_agrees_with_torch_parallel_baseline(seqlen):
+    g, x = make_inputs(2, 4, seqlen, torch.float32, seed=seqlen + 2)
+    out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE))
+    base = oracle.parallel_scan_torch(g.double(), x.double())
+    torch.testing.assert_close(out.double().cpu(), base, **REF_TOL[torch.float32])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("seqlen", [32, 128, 512, 2048, 8192, 65536])
+def test_backward_matches_oracle(dtype, seqlen):
+    g, x = make_inputs(2, 4, seqlen, dtype, seed=seqlen + 3)
+    w = torch.randn(g.shape, generator=torch.Generator().manual_seed(seqlen + 4))
+    gd = g.to(DEVICE).requires_grad_()
+    xd = x.to(DEVICE).requires_grad_()
+    out = fpscan_amd.pscan(gd, xd)
+    (out * w.to(DEVICE, dtype)).sum().backward()
+    y_ref = oracle.scan_f64(g, x)
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g, y_ref, w.to(dtype))
+    check(xd.grad, gx_ref, dtype, f"grad_tokens {dtype} L{seqlen}")
+    check(gd.grad, gg_ref, dtype, f"grad_gates {dtype} L{seqlen}")
+
+
+def test_non_power_of_two_seqlen_raises():
+    g, x = make_inputs(1, 1, 32, torch.float32)
+    with pytest.raises(RuntimeError):
+        fpscan_amd.scan_forward(g[..., :30].contiguous().to(DEVICE),
+                                x[..., :30].contiguous().to(DEVICE))
+
+
+def test_non_contiguous_raises():
+    g, x = make_inputs(2, 4, 64, torch.float32)
+    with pytest.raises(RuntimeError):
+        fpscan_amd.scan_forward(g.to(DEVICE).transpose(1, 2), x.to(DEVICE).transpose(1, 2))
+
+
+# ------------------------------------------------------------------ known answers
+def _golden(case, key):
+    rows = [[float(Fraction(v)) for v in r] for r in case[key]]
+    return torch.tensor(rows, dtype=torch.float64).unsqueeze(0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_known_answers_bit_exact(known_answers, dtype):
+    """Integer-valued cases (all-ones of scans/full_scan.py, segmented cumulative sums):
+    exact in every dtype and every combine order, so the kernel must match bit for bit."""
+    for case in known_answers:
+        if case["name"].startswith("dyadic"):
+            continue
+        g = _golden(case, "gates").to(dtype)
+        x = _golden(case, "tokens").to(dtype)
+        for key, rev in (("forward", False), ("reverse", True)):
+            out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE), reverse=rev)
+            want = torch.tensor(case[key], dtype=torch.float64).unsqueeze(0).to(dtype)
+            assert bits_equal(out.cpu(), want), f"{case['name']} {key} {dtype}"
+
+
+def test_known_answers_dyadic_fp32(known_answers):
+    for case in known_answers:
+        if not case["name"].startswith("dyadic"):
+            continue
+        g = _golden(case, "gates").float().to(DEVICE)
+        x = _golden(case, "tokens").float().to(DEVICE)
+        go = _golden(case, "grad_out").float().to(DEVICE)
+        for key, rev in (("forward", False), ("reverse", True)):
+            out = fpscan_amd.scan_forward(g, x, reverse=rev)
+            want = np.array(case[key])[None]
+            assert oracle.normwise_error(out, want) < 1e-6, f"{case['name']} {key}"
+        y = fpscan_amd.scan_forward(g, x)
+        gg, gx = fpscan_amd.scan_backward(g, y, go)
+        assert oracle.normwise_error(gx, np.array(case["grad_tokens"])[None]) < 1e-6
+        assert oracle.normwise_error(gg, np.array(case["grad_gates"])[None]) < 1e-6
+
+
+# ------------------------------------------------------------------ agreement with the
+# reference kernel's own arithmetic
+@pytest.mark.parametrize("seqlen", [32, 64, 1024, 8192, 65536])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_no_less_accurate_than_reference_kernel(seqlen, reverse):
+    g, x = make_inputs(2, 8, seqlen, torch.float32, seed=seqlen + 11)
+    out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE), reverse=reverse)
+    exact = oracle.scan_f64(g, x, reverse)
+    ref_kernel = oracle.refkernel_f32(g, x, reverse)
+    ours = oracle.normwise_error(out, exact)
+    theirs = oracle.normwise_error(ref_kernel, exact)
+    assert oracle.normwise_error(out, ref_kernel) < 1e-5
+    assert ours <= 4 * theirs + 1e-7, f"ours {ours:.2e} vs reference kernel {theirs:.2e}"
+
+
+# ------------------------------------------------------------------ edge cases
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("seqlen", [32, 64, 128, 256, 512, 4096, 65536])
+def test_ragged_row_counts(dtype, seqlen):
+    """3 x 5 = 15 rows: not a multiple of the rows per block or per wave."""
+    g, x = make_inputs(3, 5, seqlen, dtype, seed=7 * seqlen)
+    out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE))
+    check(out, oracle.scan_f64(g, x), dtype, "ragged")
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(5)).to(dtype)
+    gg, gx = fpscan_amd.scan_backward(g.to(DEVICE), out, go.to(DEVICE))
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g, out.cpu(), go)
+    check(gx, gx_ref, dtype, "ragged grad_tokens")
+    check(gg, gg_ref, dtype, "ragged grad_gates")
+
+
+@pytest.mark.parametrize("shape", [(0, 4, 64), (2, 0, 64), (0, 0, 32)])
+def test_empty_tensors(shape):
+    g = torch.rand(shape, device=DEVICE)
+    out = fpscan_amd.scan_forward(g, g.clone())
+    assert out.shape == shape
+    gg, gx = fpscan_amd.scan_backward(g, g.clone(), g.clone())
+    assert gg.shape == gx.shape == shape
+
+
+@pytest.mark.parametrize("seqlen", [32, 512])
+def test_dim_beyond_grid_y_limit(seqlen):
+    """dim > 65535 failed in the reference (gridDim.y); rows here are a 1-d range."""
+    g, x = make_inputs(1, 70000, seqlen, torch.float32, seed=3)
+    out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE))
+    check(out, oracle.scan_f64(g, x), torch.float32, "dim 70000")
+
+
+def test_out_parameter_is_written_and_returned():
+    g, x = make_inputs(2, 4, 1024, torch.float32, seed=9)
+    out = torch.full((2, 4, 1024), float("nan"), device=DEVICE)
+    ret = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE), out=out)
+    assert ret is out
+    check(out, oracle.scan_f64(g, x), torch.float32, "out=")
+
+
+def test_in_place_on_tokens():
+    g, x = make_inputs(2, 4, 4096, torch.bfloat16, seed=10)
+    xd = x.to(DEVICE)
+    fpscan_amd.scan_forward(g.to(DEVICE), xd, out=xd)
+    check(xd, oracle.scan_f64(g, x), torch.bfloat16, "in place")
+
+
+@pytest.mark.parametrize("bad", ["dtype_mix", "shape_mix", "out_dtype", "out_shape", "dim2",
+                                 "cpu_mix", "int_dtype", "out_noncontig"])
+def test_validation_errors(bad):
+    g, x = make_inputs(2, 4, 64, torch.float32)
+    g, x = g.to(DEVICE), x.to(DEVICE)
+    out = None
+    if bad == "dtype_mix":
+        g = g.half()
+    elif bad == "shape_mix":
+        g = g[:1].contiguous()
+    elif bad == "out_dtype":
+        out = torch.empty_like(x, dtype=torch.float16)
+    elif bad == "out_shape":
+        out = torch.empty(2, 4, 32, device=DEVICE)
+    elif bad == "dim2":
+        g, x = g[0], x[0]
+    elif bad == "cpu_mix":
+        g = g.cpu()
+    elif bad == "int_dtype":
+        g, x = g.int(), x.int()
+    elif bad == "out_noncontig":
+        out = torch.empty(2, 64, 4, device=DEVICE).transpose(1, 2)
+    with pytest.raises(RuntimeError):
+        fpscan_amd.scan_forward(g, x, out=out)
+
+
+def test_backward_rejects_aliased_outputs():
+    g, x = make_inputs(1, 4, 64, torch.float32)
+    g, x = g.to(DEVICE), x.to(DEVICE)
+    y = fpscan_amd.scan_forward(g, x)
+    go = torch.randn_like(y)
+    with pytest.raises(RuntimeError):
+        fpscan_amd.scan_backward(g, y, go, grad_gates=go)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("seqlen", [64, 4096, 65536])
+def test_first_processed_gate_is_ignored(dtype, seqlen):
+    """full_scan.cu:96: the first element's gate (gates[0] forward, gates[L-1] reverse) is
+    replaced by 1, so even NaN there leaves the result finite and unchanged."""
+    g, x = make_inputs(2, 4, seqlen, dtype, seed=seqlen)
+    base_f = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE))
+    base_r = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE), reverse=True)
+    gf, gr = g.clone(), g.clone()
+    gf[..., 0] = float("nan")
+    gr[..., -1] = float("nan")
+    assert bits_equal(fpscan_amd.scan_forward(gf.to(DEVICE), x.to(DEVICE)), base_f)
+    assert bits_equal(fpscan_amd.scan_forward(gr.to(DEVICE), x.to(DEVICE), reverse=True), base_r)
+
+
+def test_runs_on_the_current_stream():
+    g, x = make_inputs(4, 64, 8192, torch.float32, seed=12)
+    gd, xd = g.to(DEVICE), x.to(DEVICE)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        out = fpscan_amd.scan_forward(gd, xd)
+        ev = torch.cuda.Event()
+        ev.record(side)
+    ev.synchronize()
+    check(out, oracle.scan_f64(g, x), torch.float32, "side stream")
+
+
+@pytest.mark.parametrize("waves,ring", [(w, u) for w in (1, 2, 4, 8, 16) for u in (1, 2, 4)])
+def test_every_launch_shape(waves, ring):
+    """All (waves per row, ring depth) variants: exact on integer data, oracle-close on random
+    data, forward, reverse and backward, every dtype."""
+    try:
+        ops.set_launch_override(waves, ring)
+        for dtype in DTYPES:
+            L = 32768 if dtype == torch.float32 else 65536  # >= 16 sub-chunks per row
+            gen = torch.Generator().manual_seed(waves * 10 + ring)
+            gi = (torch.randint(0, 16, (1, 3, L), generator=gen) > 0).to(dtype)
+            xi = torch.randint(-3, 4, (1, 3, L), generator=gen).to(dtype)
+            for rev in (False, True):
+                out = fpscan_amd.scan_forward(gi.to(DEVICE), xi.to(DEVICE), reverse=rev)
+                want = torch.from_numpy(oracle.scan_f64(gi, xi, rev))
+                if dtype == torch.float32 or want.abs().max() < 256:
+                    assert bits_equal(out.cpu(), want.to(dtype)), (dtype, rev)
+            g, x = make_inputs(1, 3, L, dtype, seed=waves + ring)
+            out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE))
+            check(out, oracle.scan_f64(g, x), dtype, f"W{waves} U{ring} fwd")
+            go = torch.randn(g.shape, generator=gen).to(dtype)
+            gg, gx = fpscan_amd.scan_backward(g.to(DEVICE), out, go.to(DEVICE))
+            gg_ref, gx_ref = oracle.scan_bwd_f64(g, out.cpu(), go)
+            check(gx, gx_ref, dtype, f"W{waves} U{ring} grad_tokens")
+            check(gg, gg_ref, dtype, f"W{waves} U{ring} grad_gates")
+    finally:
+        ops.set_launch_override(0, 0)
+
+
+# ------------------------------------------------------------------ size-independent,
+# bit-exact properties
+def _properties(g, x, go, rows_checked=0):
+    """Checks at any size: (1) reverse == flip(forward(flip)); (2) tokens*2 -> out*2 exactly;
+    (3) grad_tokens == reverse scan of the shifted gates, bit for bit, and for fp32
+    grad_gates == out[t-1] * grad_tokens bit for bit."""
+    dtype = g.dtype
+    out = fpscan_amd.scan_forward(g, x)
+    rev = fpscan_amd.scan_forward(g, x, reverse=True)
+    assert bits_equal(rev, fpscan_amd.scan_forward(g.flip(-1), x.flip(-1)).flip(-1))
+    assert bits_equal(fpscan_amd.scan_forward(g, x * 2), out * 2)
+    gg, gx = fpscan_amd.scan_backward(g, out, go)
+    shifted = torch.cat([g[..., 1:], torch.ones_like(g[..., :1])], dim=-1)
+    assert bits_equal(gx, fpscan_amd.scan_forward(shifted, go, reverse=True))
+    if dtype == torch.float32:
+        prev = torch.cat([torch.zeros_like(out[..., :1]), out[..., :-1]], dim=-1)
+        assert bits_equal(gg, prev * gx)
+    if rows_checked:
+        rows = g.shape[0] * g.shape[1]
+        idx = torch.linspace(0, rows - 1, rows_checked).long()
+        L = g.shape[-1]
+        gs = g.reshape(rows, L)[idx].cpu()
+        xs = x.reshape(rows, L)[idx].cpu()
+        gos = go.reshape(rows, L)[idx].cpu()
+        y_ref = oracle.scan_f64(gs, xs)
+        check(out.reshape(rows, L)[idx], y_ref, dtype, "subset out")
+        check(rev.reshape(rows, L)[idx], oracle.scan_f64(gs, xs, True), dtype, "subset rev")
+        gg_ref, gx_ref = oracle.scan_bwd_f64(gs, y_ref, gos)
+        check(gx.reshape(rows, L)[idx], gx_ref, dtype, "subset grad_tokens")
+        check(gg.reshape(rows, L)[idx], gg_ref, dtype, "subset grad_gates")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_properties_mid_size(dtype):
+    g, x = make_inputs(2, 64, 16384, dtype, seed=21)
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(22)).to(dtype)
+    _properties(g.to(DEVICE), x.to(DEVICE), go.to(DEVICE), rows_checked=16)
+
+
+# ------------------------------------------------------------------ BASELINE configs
+def test_config1_b2_d256_l1024_fp32():
+    g, x = make_inputs(2, 256, 1024, torch.float32, seed=0)
+    check(fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE)), oracle.scan_f64(g, x),
+          torch.float32, "config 1")
+
+
+@pytest.mark.parametrize("seqlen", ALL_SEQLENS)
+def test_config2_sweep_b2_d256_fp32(seqlen):
+    g, x = make_inputs(2, 256, seqlen, torch.float32, seed=seqlen)
+    gd, xd = g.to(DEVICE), x.to(DEVICE)
+    check(fpscan_amd.scan_forward(gd, xd), oracle.scan_f64(g, x), torch.float32, "c2 fwd")
+    check(fpscan_amd.scan_forward(gd, xd, reverse=True), oracle.scan_f64(g, x, True),
+          torch.float32, "c2 rev")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_config3_b4_d512_l8192_fwd_bwd(dtype):
+    g, x = make_inputs(4, 512, 8192, dtype, seed=3)
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(33)).to(dtype)
+    gd = g.to(DEVICE).requires_grad_()
+    xd = x.to(DEVICE).requires_grad_()
+    out = fpscan_amd.pscan(gd, xd)
+    gg, gx = torch.autograd.grad(out, (gd, xd), go.to(DEVICE))
+    y_ref = oracle.scan_f64(g, x)
+    check(out, y_ref, dtype, "c3 out")
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g, y_ref, go)
+    check(gx, gx_ref, dtype, "c3 grad_tokens")
+    check(gg, gg_ref, dtype, "c3 grad_gates")
+
+
+def _bench_inputs(batch, dim, seqlen, dtype, dist, seed):
+    import bench
+
+    return bench.make_inputs(batch, dim, seqlen, dtype, dist, seed=seed, device=DEVICE)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_config4_headline_b8_d1024_l65536(dtype):
+    g, x, go = _bench_inputs(8, 1024, 65536, dtype, "mamba", seed=4)
+    _properties(g, x, go, rows_checked=48)
+
+
+def test_config5_b64_d4096_l256_and_transposed_layout():
+    g, x, go = _bench_inputs(64, 4096, 256, torch.float32, "sigmoid", seed=5)
+    out = fpscan_amd.scan_forward(g, x)
+    check(out, oracle.scan_f64(g, x), torch.float32, "c5")
+    # (batch, seqlen, dim) data: transpose in and out around the call (README.md:94-99)
+    gt, xt = g.mT.contiguous(), x.mT.contiguous()
+    out_t = fpscan_amd.scan_forward(gt.mT.contiguous(), xt.mT.contiguous()).mT.contiguous()
+    assert bits_equal(out_t, out.mT.contiguous())
+    gg, gx = fpscan_amd.scan_backward(g, out, go)
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g, out, go)
+    check(gx, gx_ref, torch.float32, "c5 grad_tokens")
+    check(gg, gg_ref, torch.float32, "c5 grad_gates")
