@@ -11,8 +11,10 @@
 // Every check runs before any HIP call, so a bad call raises RuntimeError on any machine.
 #include <torch/extension.h>
 
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+// torch-ROCm exposes HIP devices as device type "cuda"; the guard and stream accessors that
+// accept such devices are the MasqueradingAsCUDA variants
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <string>
 
@@ -68,8 +70,8 @@ at::Tensor fullscan_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at
   check_seqlen(Bx.size(2));
   if (Bx.numel() == 0) return out;
 
-  c10::hip::HIPGuard guard(Bx.device());
-  void* stream = c10::hip::getCurrentHIPStream(Bx.device().index()).stream();
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
+  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(Bx.device().index()).stream();
   // contiguous (batch, dim, seqlen): the packed strides (torch may report any stride for a
   // size-1 dimension of a contiguous tensor)
   const int64_t L = Bx.size(2), D = Bx.size(1);
@@ -108,8 +110,9 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward(const at::Tensor& gates,
   TORCH_CHECK(grad_gates.data_ptr() != grad_tokens.data_ptr(),
               "grad_gates and grad_tokens must be distinct");
 
-  c10::hip::HIPGuard guard(gates.device());
-  void* stream = c10::hip::getCurrentHIPStream(gates.device().index()).stream();
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(gates.device());
+  void* stream =
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(gates.device().index()).stream();
   const int status = fpscan_scan_bwd(gates.data_ptr(), out.data_ptr(), grad_out.data_ptr(),
                                      grad_gates.data_ptr(), grad_tokens.data_ptr(),
                                      gates.size(0), gates.size(1), gates.size(2),

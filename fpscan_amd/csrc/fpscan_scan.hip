@@ -49,10 +49,6 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 struct F32 {
   static constexpr int V = 4;
   static constexpr int kSize = 4;
-  // default sub-chunks in flight per wave (W == 1): the deepest ring that keeps the
-  // forward / backward kernel within 64 VGPRs, i.e. 8 waves per SIMD
-  static constexpr int kRingFwd = 4;
-  static constexpr int kRingBwd = 2;
   __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
@@ -68,14 +64,13 @@ struct F32 {
 struct F16 {
   static constexpr int V = 8;
   static constexpr int kSize = 2;
-  // default sub-chunks in flight per wave (W == 1): the deepest ring that keeps the
-  // forward / backward kernel within 64 VGPRs, i.e. 8 waves per SIMD
-  static constexpr int kRingFwd = 4;
-  static constexpr int kRingBwd = 2;
   __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const f16x2 h = __builtin_bit_cast(f16x2, v[i]);
+      // copy the element out first: a bit_cast of the vector-element lvalue v[i] reads
+      // element 0 for every i with this compiler
+      const unsigned int word = v[i];
+      const f16x2 h = __builtin_bit_cast(f16x2, word);
       f[2 * i] = static_cast<float>(h.x);
       f[2 * i + 1] = static_cast<float>(h.y);
     }
@@ -99,10 +94,6 @@ struct F16 {
 struct BF16 {
   static constexpr int V = 8;
   static constexpr int kSize = 2;
-  // default sub-chunks in flight per wave (W == 1): the deepest ring that keeps the
-  // forward / backward kernel within 64 VGPRs, i.e. 8 waves per SIMD
-  static constexpr int kRingFwd = 2;
-  static constexpr int kRingBwd = 1;
   __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -241,7 +232,7 @@ __device__ __forceinline__ void st16(void* base, int64_t elem, int size, u32x4 v
 // the hardware range check turns any offset outside the row into a zero read / dropped
 // write instead of a fault.
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
-constexpr int kCacheNT = 2;             // cache-policy bit: nontemporal (streaming) store
+constexpr int kCacheNT = 2;             // cache-policy bit: nontemporal (streamed once)
 
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
@@ -250,8 +241,9 @@ __device__ __forceinline__ Rsrc row_rsrc(const void* p, int64_t row_base, int si
       const_cast<char*>(static_cast<const char*>(p)) + row_base * size, (short)0, bytes, kRsrcWord3);
 }
 
+// Every element is read once: the 16-byte operand loads are nontemporal, like the stores.
 __device__ __forceinline__ u32x4 bld16(Rsrc r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCacheNT));
 }
 
 __device__ __forceinline__ void bst16(Rsrc r, uint32_t off, u32x4 v) {
@@ -542,30 +534,8 @@ __global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
 // ---------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------
-constexpr int kMaxDevices = 64;
-std::atomic<int> g_cu_count[kMaxDevices];
 std::atomic<int> g_override_w{0};
 std::atomic<int> g_override_u{0};
-
-int cu_count(int* status) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
-    *status = FPSCAN_ERR_DEVICE;
-    return 0;
-  }
-  if (dev < kMaxDevices) {
-    const int cached = g_cu_count[dev].load(std::memory_order_relaxed);
-    if (cached > 0) return cached;
-  }
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus <= 0) {
-    *status = FPSCAN_ERR_DEVICE;
-    return 0;
-  }
-  if (dev < kMaxDevices) g_cu_count[dev].store(cus, std::memory_order_relaxed);
-  return cus;
-}
 
 int launch(const void* kernel, int64_t groups, int threads, const Args& a, hipStream_t stream) {
   // One group per block; very large problems loop inside the kernel (grid-stride) so the
@@ -611,8 +581,9 @@ const void* short_kernel(int g) {
   }
 }
 
-// Chooses the launch for one problem. Rows are independent; a row is owned by W waves so
-// that rows * W reaches one full occupancy round of the device (32 waves per CU).
+// Chooses the launch for one problem. Rows are independent; long rows are owned by W waves
+// (W = 16 when the row has at least 16 sub-chunks) with U sub-chunks in flight per wave. The
+// ring depths are the deepest that keep every variant within 64 VGPRs (8 waves per SIMD).
 template <class E, int kMode>
 int run(const Args& a, hipStream_t stream) {
   constexpr int V = E::V;
@@ -624,15 +595,13 @@ int run(const Args& a, hipStream_t stream) {
     return launch(short_kernel<E, kMode>(g), (a.rows + rows_per_block - 1) / rows_per_block,
                   256, a, stream);
   }
-  int status = FPSCAN_OK;
-  const int cus = cu_count(&status);
-  if (status != FPSCAN_OK) return status;
   const int nsub = L / kSub;
-  const int64_t target_waves = (int64_t)cus * 32;
-  int w = 1;
-  while (w < 16 && 2 * w <= nsub && a.rows * w < target_waves) w *= 2;
-  int u_max = (kMode == kBwd) ? E::kRingBwd : E::kRingFwd;
-  if (w > 1 && u_max > 2) u_max = 2;
+  // Up to 16 waves share a row: each round then touches W KiB of each tensor contiguously
+  // and 16x fewer rows are in flight than with one wave per row, which is what the HBM
+  // controllers and address translation reward. Few-row problems also fill the device this
+  // way (rows * 16 waves).
+  int w = nsub < 16 ? nsub : 16;
+  int u_max = (w == 1 && kMode != kBwd) ? 4 : 2;
   const int ow = g_override_w.load(std::memory_order_relaxed);
   const int ou = g_override_u.load(std::memory_order_relaxed);
   if (ow > 0) w = ow <= nsub ? ow : nsub;

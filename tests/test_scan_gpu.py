@@ -318,7 +318,15 @@ def _properties(g, x, go, rows_checked=0):
     out = fpscan_amd.scan_forward(g, x)
     rev = fpscan_amd.scan_forward(g, x, reverse=True)
     assert bits_equal(rev, fpscan_amd.scan_forward(g.flip(-1), x.flip(-1)).flip(-1))
-    assert bits_equal(fpscan_amd.scan_forward(g, x * 2), out * 2)
+    # doubling commutes with rounding except for fp16 subnormal results (fixed spacing below
+    # 2^-14; bf16 and fp32 share fp32's exponent range): fp16 compares normal elements only
+    y2 = fpscan_amd.scan_forward(g, x * 2)
+    if dtype == torch.float16:
+        normal = out.abs() >= 2.0 ** -13
+        assert normal.float().mean() > 0.5
+        assert bits_equal(y2[normal], (out * 2)[normal])
+    else:
+        assert bits_equal(y2, out * 2)
     gg, gx = fpscan_amd.scan_backward(g, out, go)
     shifted = torch.cat([g[..., 1:], torch.ones_like(g[..., :1])], dim=-1)
     assert bits_equal(gx, fpscan_amd.scan_forward(shifted, go, reverse=True))
