@@ -335,6 +335,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--launch", default=None, help="waves_per_row,ring_depth override")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run 5 device copies of a 1 GiB buffer: the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -352,6 +355,13 @@ def main():
         w, u = (int(v) for v in args.launch.split(","))
         ops.set_launch_override(w, u)
 
+    if args.calibrate_copy:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.workload == "c4":
         res = bench_headline(args)
     elif args.workload == "c2":
