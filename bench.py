@@ -219,6 +219,10 @@ def bench_headline(args):
     achieved = bwd_bytes / (bwd_avg / 1e3) / 1e9
     traffic, traffic_src = load_traffic(args.workload, SHORT[dtype])
     value = 8 * N * s / (ms_per_step / 1e3) / 1e9
+    dcode = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+    tiled = fpscan_amd.ops._load_extension().workspace_bytes(B, D, L, dcode, 1) > 0
+    bwd_kernel = ("scan_tiles<bwd> (fused backward, persistent tiles with look-back)" if tiled
+                  else "scan_long_rows<bwd> (fused backward, one block per row)")
 
     res = {
         "metric": METRIC,
@@ -252,7 +256,7 @@ def bench_headline(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": "scan_long_rows<bwd> (fused backward)",
+            "kernel": bwd_kernel,
             "algorithmic_bytes_per_launch": bwd_bytes,
             "traffic_source": traffic_src,
         },

@@ -55,6 +55,13 @@ void check_seqlen(int64_t seqlen) {
               "seqlen must be a power of 2, >= 32, <= 65536, got ", seqlen);
 }
 
+// Tile-status workspace from torch's caching allocator on the tensors' device (the call is
+// made with that device current); an empty tensor when the problem needs none.
+at::Tensor workspace(size_t bytes, const at::Tensor& like) {
+  if (bytes == 0) return at::Tensor();
+  return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
+}
+
 void check_status(int status) {
   TORCH_CHECK(status == FPSCAN_OK, "fpscan: ", fpscan_strerror(status), " (status ", status,
               ")");
@@ -75,10 +82,12 @@ at::Tensor fullscan_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at
   // contiguous (batch, dim, seqlen): the packed strides (torch may report any stride for a
   // size-1 dimension of a contiguous tensor)
   const int64_t L = Bx.size(2), D = Bx.size(1);
+  const int dt = dtype_code(Bx.scalar_type());
+  const size_t ws_bytes = fpscan_workspace_bytes(Bx.size(0), D, L, dt, FPSCAN_OP_FWD);
+  at::Tensor ws = workspace(ws_bytes, Bx);
   const int status = fpscan_scan_fwd(Ax.data_ptr(), Bx.data_ptr(), out.data_ptr(), Bx.size(0),
-                                     D, L, D * L, L,
-                                     dtype_code(Bx.scalar_type()), reverse ? 1 : 0, nullptr, 0,
-                                     stream);
+                                     D, L, D * L, L, dt, reverse ? 1 : 0,
+                                     ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
   check_status(status);
   return out;
 }
@@ -113,11 +122,15 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward(const at::Tensor& gates,
   c10::hip::HIPGuardMasqueradingAsCUDA guard(gates.device());
   void* stream =
       c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(gates.device().index()).stream();
+  const int dt = dtype_code(gates.scalar_type());
+  const size_t ws_bytes =
+      fpscan_workspace_bytes(gates.size(0), gates.size(1), gates.size(2), dt, FPSCAN_OP_BWD);
+  at::Tensor ws = workspace(ws_bytes, gates);
   const int status = fpscan_scan_bwd(gates.data_ptr(), out.data_ptr(), grad_out.data_ptr(),
                                      grad_gates.data_ptr(), grad_tokens.data_ptr(),
                                      gates.size(0), gates.size(1), gates.size(2),
-                                     gates.size(1) * gates.size(2), gates.size(2),
-                                     dtype_code(gates.scalar_type()), nullptr, 0, stream);
+                                     gates.size(1) * gates.size(2), gates.size(2), dt,
+                                     ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
   check_status(status);
   return {grad_gates, grad_tokens};
 }
@@ -143,4 +156,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "tuning hook: force waves per row / ring depth (0 = built-in choice)",
         pybind11::arg("waves_per_row"), pybind11::arg("ring_depth"));
   m.def("abi_version", []() { return fpscan_abi_version(); });
+  m.def("set_tiling", [](int mode) {
+    TORCH_CHECK(fpscan_set_tiling(mode) == FPSCAN_OK, "tiling mode must be 0, 1 or 2");
+  }, "path selection: 0 automatic, 1 row streaming only, 2 tiled whenever possible",
+        pybind11::arg("mode"));
+  m.def("workspace_bytes", &fpscan_workspace_bytes, pybind11::arg("batch"),
+        pybind11::arg("dim"), pybind11::arg("seqlen"), pybind11::arg("dtype"),
+        pybind11::arg("op"));
 }

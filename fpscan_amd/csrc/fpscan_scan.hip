@@ -49,6 +49,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 struct F32 {
   static constexpr int V = 4;
   static constexpr int kSize = 4;
+  static constexpr int kSlot = 0;  // index of this type in per-type tables
   __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
@@ -64,6 +65,7 @@ struct F32 {
 struct F16 {
   static constexpr int V = 8;
   static constexpr int kSize = 2;
+  static constexpr int kSlot = 1;  // index of this type in per-type tables
   __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -94,6 +96,7 @@ struct F16 {
 struct BF16 {
   static constexpr int V = 8;
   static constexpr int kSize = 2;
+  static constexpr int kSlot = 2;  // index of this type in per-type tables
   __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -136,6 +139,16 @@ __device__ __forceinline__ float dpp(float old, float src) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
                                          kCtrl, kRowMask, 0xf, false));
+}
+
+// Workgroup barrier that orders LDS only. __syncthreads() is a workgroup-scope fence on all
+// memory, which on gfx9 waits for every outstanding global load -- it would drain the operand
+// ring at each barrier. The barriers here guard LDS exchanges only: operands are read-only
+// and every output element is written by the lane that read its inputs.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ __forceinline__ float readlane(float v, int lane) {
@@ -450,7 +463,7 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         } else {
           // the W sub-chunk aggregates of this round, scanned across lanes 0..W-1 (one DPP row)
           if (lane == 63) exch[r & 1][w] = f32x2{A, B};
-          __syncthreads();
+          lds_barrier();
           float eA = 1.0f, eB = 0.0f;
           if (lane < W) {
             const f32x2 t = exch[r & 1][lane];
@@ -476,6 +489,261 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         // above this slot's refill, which turns every wait into a wait for all loads
         __builtin_amdgcn_sched_barrier(0);
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Long rows, tiled: a persistent, co-resident grid walks tiles in memory order.
+//
+// A tile is TW consecutive sub-chunks of one row (TW KiB of each tensor), handled by one
+// workgroup of TW waves; workgroup b takes tiles b, b + G, b + 2G, ... (G = grid size), so
+// the tiles in flight at any moment form one contiguous window of each tensor -- the access
+// pattern of a plain streaming kernel. Tiles of one row are chained by a decoupled look-back:
+//   1. each tile reduces its own data to one affine map (A, B) and publishes it at once as
+//      one 64-bit word in `status` (B in the high half, A in the low half; all-ones = not yet
+//      published; NaNs are canonicalised so all-ones never occurs as data);
+//   2. the carry into the tile is the composition of the words of all preceding tiles of the
+//      row (a row has at most 64 tiles, so one wave scan over 64 lanes covers them; tiles
+//      before the row start enter as the constant map 0, i.e. the zero initial state);
+//   3. the tile applies that carry and stores.
+// The look-back is deferred by one tile to keep its coherent-load latency off the critical
+// path: after reducing and publishing tile k, wave 0 loads tile k's predecessor words (before
+// issuing the next operand loads, since vector loads complete in issue order); the workgroup
+// then reduces tile k+1 and only after that uses the words to finish tile k. A ring of three
+// tiles per workgroup (k finishing, k+1 reducing, k+2 in flight) holds the operands.
+// Publishing never waits, so the dependencies are acyclic: with every workgroup resident
+// (cooperative launch), the workgroup owning the lowest unpublished tile only ever waits on
+// lower tiles, which are published, and makes progress. Each wait is also bounded; a wait
+// that exceeds the bound (which a correct launch never reaches) bumps the overrun word after
+// the status array and proceeds, so the kernel always terminates.
+// ---------------------------------------------------------------------------------------
+constexpr uint64_t kNotPublished = ~0ull;
+constexpr int kSpinLimit = 1 << 16;  // polls of ~1 us each (a device-coherent load)
+
+__device__ __forceinline__ uint32_t canonical_bits(float v) {
+  return v != v ? 0x7fc00000u : __float_as_uint(v);
+}
+
+__device__ __forceinline__ uint64_t pack_map(float A, float B) {
+  return ((uint64_t)canonical_bits(B) << 32) | canonical_bits(A);
+}
+
+__global__ void __launch_bounds__(256) clear_status(uint64_t* __restrict__ status, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    status[i] = (i == n - 1) ? 0ull : kNotPublished;  // the last word counts wait overruns
+}
+
+// Per-slot state of the tile ring: the tile, its row resources, its segment in the row and
+// the operands of this wave's sub-chunk.
+template <int kMode>
+struct TileSlot {
+  Slot<kMode> data;
+  RowRsrc<kMode> rr;
+  int64_t tile;
+  int seg;
+};
+
+// Status words go through a buffer resource too: every lane and wave issues the same
+// instructions, and the ones that must not touch memory use kNoOffset (reads return 0, writes
+// are dropped). Straight-line code keeps the compiler's wait counts partial, which is what
+// keeps the operand ring in flight. The cache policy is the device-coherent one (sc1), the
+// same instruction an agent-scope relaxed atomic load/store of 64 bits compiles to here.
+constexpr int kCacheCoherent = 16;
+
+__device__ __forceinline__ uint64_t status_load(Rsrc r, uint32_t off) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCacheCoherent));
+  return ((uint64_t)v.y << 32) | v.x;
+}
+
+__device__ __forceinline__ void status_store(Rsrc r, uint32_t off, uint64_t word) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  u32x2 v;
+  v.x = (uint32_t)word;
+  v.y = (uint32_t)(word >> 32);
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kCacheCoherent);
+}
+
+template <class E, int kMode, int TW>
+__device__ __forceinline__ void tile_setup(const Args& a, TileSlot<kMode>& ts, int64_t tile,
+                                           int64_t ntiles, int tpr_log2, int w, uint32_t lane_off) {
+  constexpr int kSub = 64 * E::V;
+  constexpr bool kReverse = kMode != kFwd;
+  ts.tile = tile;
+  const bool live = tile < ntiles;
+  const int64_t row = live ? (tile >> tpr_log2) : 0;
+  ts.seg = live ? (int)(tile & ((1 << tpr_log2) - 1)) : 0;
+  const int64_t base = row_offset(a, row);
+  const int row_bytes = a.seqlen * E::kSize;
+  ts.rr.in0 = row_rsrc(a.in0, base, E::kSize, row_bytes);
+  ts.rr.in1 = row_rsrc(a.in1, base, E::kSize, row_bytes);
+  ts.rr.out0 = row_rsrc(a.out0, base, E::kSize, row_bytes);
+  if constexpr (kMode == kBwd) {
+    ts.rr.in2 = row_rsrc(a.in2, base, E::kSize, row_bytes);
+    ts.rr.out1 = row_rsrc(a.out1, base, E::kSize, row_bytes);
+  }
+  const int nsub = a.seqlen / kSub;
+  const int j = ts.seg * TW + w;
+  const uint32_t sb = live ? (uint32_t)((kReverse ? nsub - 1 - j : j) * kSub * E::kSize) : kNoOffset;
+  load_slot<E, kMode>(ts.rr, ts.data, sb, lane_off);
+}
+
+// The affine maps of this wave's sub-chunk of a tile, in processing order (see make_maps);
+// returns the sub-chunk's byte offset in its row.
+template <class E, int kMode, int TW>
+__device__ __forceinline__ uint32_t tile_maps(const TileSlot<kMode>& ts, int nsub, int row_bytes,
+                                              int w, int lane, float (&al)[E::V],
+                                              float (&be)[E::V], float (&ysh)[E::V]) {
+  constexpr int kSub = 64 * E::V;
+  constexpr bool kReverse = kMode != kFwd;
+  const int j = ts.seg * TW + w;
+  const uint32_t sb = (uint32_t)((kReverse ? nsub - 1 - j : j) * kSub * E::kSize);
+  float gate_next = 1.0f, out_prev = 0.0f;
+  if constexpr (kMode == kBwd) {
+    gate_next = (sb + kSub * E::kSize < (uint32_t)row_bytes) ? ts.data.gate_after : 1.0f;
+    out_prev = (sb > 0) ? ts.data.out_before : 0.0f;
+  }
+  make_maps<E, kMode>(ts.data, al, be, ysh, gate_next, out_prev, lane == 0, lane == 63);
+  if (kMode != kBwd && j == 0 && lane == 0) al[0] = 1.0f;  // full_scan.cu:96
+  return sb;
+}
+
+template <class E, int kMode, int TW>
+__global__ void __launch_bounds__(64 * TW)
+scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, const int64_t ntiles) {
+  constexpr int V = E::V;
+  constexpr int kSub = 64 * V;
+  constexpr bool kReverse = kMode != kFwd;
+
+  __shared__ f32x2 exch[TW];
+  __shared__ float tile_carry;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int vec = kReverse ? 63 - lane : lane;
+  const uint32_t lane_off = (uint32_t)vec * 16u;
+  const int nsub = a.seqlen / kSub;
+  const int row_bytes = a.seqlen * E::kSize;
+  const int64_t G = gridDim.x;
+  const Rsrc st = __builtin_amdgcn_make_buffer_rsrc(status, (short)0,
+                                                    (int)((ntiles + 1) * sizeof(uint64_t)),
+                                                    kRsrcWord3);
+
+  TileSlot<kMode> ring[3];
+  tile_setup<E, kMode, TW>(a, ring[0], blockIdx.x, ntiles, tpr_log2, w, lane_off);
+  __builtin_amdgcn_sched_barrier(0);
+  tile_setup<E, kMode, TW>(a, ring[1], blockIdx.x + G, ntiles, tpr_log2, w, lane_off);
+  __builtin_amdgcn_sched_barrier(0);
+  ring[2].tile = ntiles;  // filled with tile b + 2G at the end of the first step
+  ring[2].seg = 0;
+  ring[2].rr = ring[0].rr;
+
+  // what the previous tile's finish needs from its reduce: the lane's inclusive map, the
+  // wave's exclusive prefix inside the tile, and (wave 0) the predecessor words
+  float held_A = 1.0f, held_B = 0.0f, held_pA = 1.0f, held_pB = 0.0f;
+  uint64_t held_word = 0;
+  bool have_prev = false;
+
+  // A fixed trip count (this workgroup's tiles, plus one step that only finishes the last,
+  // rounded up to whole rings; surplus steps touch no memory) instead of an exit inside the
+  // unrolled body: with an exit there, the compiler's wait counts at the loop head collapse to
+  // waiting for every load in flight.
+  const int64_t mine = (ntiles - blockIdx.x + G - 1) / G;
+  const int64_t steps = ((mine + 1 + 2) / 3) * 3;
+  for (int64_t k0 = 0; k0 < steps; k0 += 3) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      TileSlot<kMode>& cur = ring[u];
+      TileSlot<kMode>& prev = ring[(u + 2) % 3];
+      const bool cur_live = cur.tile < ntiles;  // uniform across the workgroup
+
+      // (1) reduce the current tile (a dead tile reduces zeros and publishes nothing)
+      float al[V], be[V], ysh[V];
+      tile_maps<E, kMode, TW>(cur, nsub, row_bytes, w, lane, al, be, ysh);
+      float A, B;
+      lane_aggregate<E>(al, be, A, B);
+      wave_scan(A, B);
+      if (lane == 63) exch[w] = f32x2{A, B};
+      lds_barrier();
+      float eA = 1.0f, eB = 0.0f;
+      if (lane < TW) {
+        const f32x2 e = exch[lane];
+        eA = e.x;
+        eB = e.y;
+      }
+      combine_from<kRowShr1>(eA, eB);
+      if constexpr (TW > 2) combine_from<kRowShr2>(eA, eB);
+      if constexpr (TW > 4) combine_from<kRowShr4>(eA, eB);
+      if constexpr (TW > 8) combine_from<kRowShr8>(eA, eB);
+      const float cur_pA = (w > 0) ? readlane(eA, w - 1) : 1.0f;
+      const float cur_pB = (w > 0) ? readlane(eB, w - 1) : 0.0f;
+      const bool publisher = cur_live && w == 0 && lane == 0;
+      status_store(st, publisher ? (uint32_t)(cur.tile * sizeof(uint64_t)) : kNoOffset,
+                   pack_map(readlane(eA, TW - 1), readlane(eB, TW - 1)));
+
+      // (2) the previous tile's carry from its predecessor words (loaded by wave 0 at the end
+      // of the previous step; other waves hold zeros and compute a carry nobody uses)
+      uint64_t word = held_word;
+      if (__builtin_amdgcn_ballot_w64(word == kNotPublished) != 0) {
+        // a predecessor was not published yet: poll (bounded). The poll is an atomic load,
+        // which the compiler must re-issue every iteration (a plain buffer load would be
+        // hoisted out of the loop).
+        const int64_t p = prev.tile - 64 + lane;
+        const bool in_row = p >= prev.tile - prev.seg;
+        for (int it = 0;; ++it) {
+          __builtin_amdgcn_s_sleep(1);
+          word = in_row ? __hip_atomic_load(status + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : 0ull;
+          if (__builtin_amdgcn_ballot_w64(word == kNotPublished) == 0) break;
+          if (it == kSpinLimit) {
+            if (lane == 0)
+              __hip_atomic_fetch_add(status + ntiles, 1ull, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+            word = 0;  // only after an overrun: keep the result finite
+            break;
+          }
+        }
+      }
+      float mA = __uint_as_float((uint32_t)word);
+      float mB = __uint_as_float((uint32_t)(word >> 32));
+      wave_scan(mA, mB);
+      if (w == 0 && lane == 63) tile_carry = mB;
+      lds_barrier();
+
+      // (3) finish the previous tile (nothing is stored on the first step)
+      {
+        const float c_tile = tile_carry;
+        const float c_in = fmaf(held_pA, c_tile, held_pB);
+        float pal[V], pbe[V], pys[V];
+        const uint32_t sb = tile_maps<E, kMode, TW>(prev, nsub, row_bytes, w, lane, pal, pbe, pys);
+        const float y_lane_end = fmaf(held_A, c_in, held_B);
+        const float y_enter = dpp<kWaveShr1>(c_in, y_lane_end);
+        u32x4 o0, o1;
+        finish_lane<E, kMode>(pal, pbe, pys, y_enter, o0, o1);
+        const uint32_t so = have_prev ? sb + lane_off : kNoOffset;
+        bst16(prev.rr.out0, so, o0);
+        if constexpr (kMode == kBwd) bst16(prev.rr.out1, so, o1);
+      }
+      held_A = A;
+      held_B = B;
+      held_pA = cur_pA;
+      held_pB = cur_pB;
+      have_prev = cur_live;
+
+      // (4) wave 0: load the current tile's predecessor words now, before the refill below:
+      // vector loads complete in issue order, so waiting for these words in the next step
+      // does not wait for the refill. By then the neighbouring workgroups, which reduce the
+      // predecessors at the same pace, have normally published them. Lanes before the row
+      // start (and all other waves) read 0: the constant map 0, the zero initial state.
+      {
+        const int64_t q = cur.tile - 64 + lane;
+        const bool mine = w == 0 && cur_live && cur.seg > 0 && q >= cur.tile - cur.seg;
+        held_word = status_load(st, mine ? (uint32_t)(q * sizeof(uint64_t)) : kNoOffset);
+      }
+      // (5) refill the finished slot with the tile three steps ahead
+      tile_setup<E, kMode, TW>(a, prev, cur.tile + 2 * G, ntiles, tpr_log2, w, lane_off);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -536,6 +804,64 @@ __global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
 // ---------------------------------------------------------------------------------------
 std::atomic<int> g_override_w{0};
 std::atomic<int> g_override_u{0};
+std::atomic<int> g_tiling{0};  // 0 automatic, 1 row streaming only, 2 tiled when possible
+
+// Tiled path geometry: TW sub-chunks per tile, at most 64 tiles per row (one look-back window)
+constexpr int kTileWaves = 16;
+// Below this many bytes per tensor the row-streaming kernels win: the persistent grid needs
+// dozens of tiles per workgroup to amortise filling and draining its three-tile pipeline
+// (measured: fp32 B2 D256 L65536, 128 MiB per tensor, streams at 5.6 TB/s and tiles at 4.4).
+constexpr int64_t kTiledMinBytes = 512ll << 20;
+
+struct TilePlan {
+  bool use;
+  int tpr;         // tiles per row
+  int64_t ntiles;  // rows * tpr
+  size_t bytes;    // workspace: one status word per tile + one overrun counter
+};
+
+// `backward` selects the plan of fpscan_scan_bwd. In automatic mode the fp32 forward/reverse
+// scan keeps streaming rows: its rows have 16 tiles, so a tile waits on a late predecessor
+// more often (15 % of tiles at B8 D1024 L65536), and the tiled path measured 4 % slower there
+// while every other large case measured 1.5-4.5 % faster.
+TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling, bool backward) {
+  TilePlan t{false, 0, 0, 0};
+  const int64_t sub = 64 * (16 / size);
+  const int64_t nsub = seqlen / sub;
+  if (tiling == 1 || nsub < kTileWaves) return t;
+  t.tpr = (int)(nsub / kTileWaves);
+  if (t.tpr > 64) return t;
+  if (tiling == 0 && rows * seqlen * size < kTiledMinBytes) return t;
+  if (tiling == 0 && size == 4 && !backward) return t;
+  t.ntiles = rows * t.tpr;
+  if ((t.ntiles + 1) * (int64_t)sizeof(uint64_t) > INT32_MAX) return t;  // status buffer range
+  t.use = true;
+  t.bytes = (size_t)(t.ntiles + 1) * sizeof(uint64_t);
+  return t;
+}
+
+constexpr int kMaxDevices = 64;
+constexpr int kTiledKernels = 9;  // 3 element types x 3 modes
+std::atomic<int> g_resident_blocks[kMaxDevices][kTiledKernels];
+
+// Workgroups of `kernel` that fit on the current device at once (CUs x blocks per CU); 0 if
+// the device cannot be queried. Cached per device and kernel.
+int resident_blocks(const void* kernel, int slot, int threads) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kMaxDevices) {
+    const int cached = g_resident_blocks[dev][slot].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+      cus <= 0 || per_cu <= 0)
+    return 0;
+  const int n = cus * per_cu;
+  if (dev < kMaxDevices) g_resident_blocks[dev][slot].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 int launch(const void* kernel, int64_t groups, int threads, const Args& a, hipStream_t stream) {
   // One group per block; very large problems loop inside the kernel (grid-stride) so the
@@ -584,11 +910,47 @@ const void* short_kernel(int g) {
 // Chooses the launch for one problem. Rows are independent; long rows are owned by W waves
 // (W = 16 when the row has at least 16 sub-chunks) with U sub-chunks in flight per wave. The
 // ring depths are the deepest that keep every variant within 64 VGPRs (8 waves per SIMD).
+// Tiled launch: clear the status words, then the persistent grid with every workgroup
+// resident (cooperative launch). Returns -1 when the device refuses the cooperative launch,
+// so that the caller can stream rows instead.
 template <class E, int kMode>
-int run(const Args& a, hipStream_t stream) {
+int run_tiled(const Args& a, const TilePlan& plan, void* workspace, hipStream_t stream, int slot) {
+  const void* kernel = reinterpret_cast<const void*>(&scan_tiles<E, kMode, kTileWaves>);
+  const int threads = 64 * kTileWaves;
+  const int resident = resident_blocks(kernel, slot, threads);
+  if (resident <= 0) return -1;
+  uint64_t* status = static_cast<uint64_t*>(workspace);
+  const int64_t nwords = plan.ntiles + 1;
+  const int64_t clear_blocks = (nwords + 255) / 256 < 1024 ? (nwords + 255) / 256 : 1024;
+  void* cargs[] = {&status, const_cast<int64_t*>(&nwords)};
+  if (hipLaunchKernel(reinterpret_cast<const void*>(&clear_status), dim3((unsigned)clear_blocks),
+                      dim3(256), cargs, 0, stream) != hipSuccess)
+    return FPSCAN_ERR_LAUNCH;
+  const int64_t grid = plan.ntiles < resident ? plan.ntiles : resident;
+  Args copy = a;
+  int tpr_log2 = 0;
+  while ((1 << tpr_log2) < plan.tpr) ++tpr_log2;
+  int64_t ntiles = plan.ntiles;
+  void* kargs[] = {&copy, &status, &tpr_log2, &ntiles};
+  const hipError_t err = hipLaunchCooperativeKernel(kernel, dim3((unsigned)grid), dim3(threads),
+                                                    kargs, 0, stream);
+  if (err == hipSuccess) return FPSCAN_OK;
+  (void)hipGetLastError();  // clear the refusal; the caller streams rows instead
+  return -1;
+}
+
+template <class E, int kMode>
+int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   constexpr int V = E::V;
   constexpr int kSub = 64 * V;
   const int L = a.seqlen;
+  const TilePlan plan =
+      plan_tiles(a.rows, L, E::kSize, g_tiling.load(std::memory_order_relaxed), kMode == kBwd);
+  if (plan.use && workspace != nullptr && ws_bytes >= plan.bytes) {
+    const int st = run_tiled<E, kMode>(a, plan, workspace, stream,
+                                       E::kSlot * 3 + kMode);
+    if (st >= 0) return st;
+  }
   if (L < kSub) {
     const int g = L / V;
     const int64_t rows_per_block = 4 * (64 / g);
@@ -613,11 +975,11 @@ int run(const Args& a, hipStream_t stream) {
 }
 
 template <int kMode>
-int dispatch(int dtype, const Args& a, hipStream_t stream) {
+int dispatch(int dtype, const Args& a, void* ws, size_t ws_bytes, hipStream_t stream) {
   switch (dtype) {
-    case FPSCAN_DTYPE_F32: return run<F32, kMode>(a, stream);
-    case FPSCAN_DTYPE_F16: return run<F16, kMode>(a, stream);
-    case FPSCAN_DTYPE_BF16: return run<BF16, kMode>(a, stream);
+    case FPSCAN_DTYPE_F32: return run<F32, kMode>(a, ws, ws_bytes, stream);
+    case FPSCAN_DTYPE_F16: return run<F16, kMode>(a, ws, ws_bytes, stream);
+    case FPSCAN_DTYPE_BF16: return run<BF16, kMode>(a, ws, ws_bytes, stream);
     default: return FPSCAN_ERR_DTYPE;
   }
 }
@@ -664,8 +1026,6 @@ extern "C" {
 int fpscan_scan_fwd(const void* gates, const void* tokens, void* out, int64_t batch, int64_t dim,
                     int64_t seqlen, int64_t stride_b, int64_t stride_d, int dtype, int reverse,
                     void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   Args a{};
   const int st = validate(batch, dim, seqlen, stride_b, stride_d, dtype, &a);
   if (st != FPSCAN_OK) return st;
@@ -676,15 +1036,14 @@ int fpscan_scan_fwd(const void* gates, const void* tokens, void* out, int64_t ba
   a.in1 = tokens;
   a.out0 = out;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return reverse ? dispatch<kRev>(dtype, a, s) : dispatch<kFwd>(dtype, a, s);
+  return reverse ? dispatch<kRev>(dtype, a, workspace, workspace_bytes, s)
+                 : dispatch<kFwd>(dtype, a, workspace, workspace_bytes, s);
 }
 
 int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out, void* grad_gates,
                     void* grad_tokens, int64_t batch, int64_t dim, int64_t seqlen,
                     int64_t stride_b, int64_t stride_d, int dtype, void* workspace,
                     size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   Args a{};
   const int st = validate(batch, dim, seqlen, stride_b, stride_d, dtype, &a);
   if (st != FPSCAN_OK) return st;
@@ -698,16 +1057,17 @@ int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out, vo
   a.in2 = out;
   a.out0 = grad_tokens;
   a.out1 = grad_gates;
-  return dispatch<kBwd>(dtype, a, static_cast<hipStream_t>(stream));
+  return dispatch<kBwd>(dtype, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype, int op) {
-  (void)batch;
-  (void)dim;
-  (void)seqlen;
-  (void)dtype;
-  (void)op;
-  return 0;
+  const int size = itemsize(dtype);
+  if (size == 0 || batch <= 0 || dim <= 0 || seqlen < 32 || seqlen > 65536 ||
+      (seqlen & (seqlen - 1)) != 0)
+    return 0;
+  const TilePlan plan = plan_tiles(batch * dim, seqlen, size,
+                                   g_tiling.load(std::memory_order_relaxed), op == FPSCAN_OP_BWD);
+  return plan.use ? plan.bytes : 0;
 }
 
 const char* fpscan_strerror(int status) {
@@ -726,6 +1086,12 @@ const char* fpscan_strerror(int status) {
 }
 
 int fpscan_abi_version(void) { return FPSCAN_ABI_VERSION; }
+
+int fpscan_set_tiling(int mode) {
+  if (mode < 0 || mode > 2) return FPSCAN_ERR_SHAPE;
+  g_tiling.store(mode, std::memory_order_relaxed);
+  return FPSCAN_OK;
+}
 
 int fpscan_set_launch_override(int waves_per_row, int ring_depth) {
   const bool w_ok = waves_per_row == 0 || waves_per_row == 1 || waves_per_row == 2 ||

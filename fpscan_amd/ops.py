@@ -110,3 +110,9 @@ def set_launch_override(waves_per_row: int = 0, ring_depth: int = 0) -> None:
     """Tuning hook: force the number of waves per row and the per-wave ring depth of the
     long-row kernels (0 restores the built-in choice). Process-wide."""
     _load_extension().set_launch_override(int(waves_per_row), int(ring_depth))
+
+
+def set_tiling(mode: int = 0) -> None:
+    """Path selection for long rows (process-wide): 0 automatic, 1 row streaming only,
+    2 tiled (persistent grid with look-back) whenever the shape allows."""
+    _load_extension().set_tiling(int(mode))

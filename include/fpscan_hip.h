@@ -16,6 +16,14 @@
  * threads. Pointers are device pointers on the current HIP device; they must be 16-byte
  * aligned and the strides must be multiples of 16 bytes (16/itemsize elements).
  *
+ * Workspace: large problems run fastest on the tiled path, which needs
+ * fpscan_workspace_bytes() bytes of device memory (one 8-byte word per tile, about 0.2 % of
+ * one tensor). Pass a buffer of at least that size, 8-byte aligned, owned by the caller and
+ * not used by any other call in flight. Its contents are overwritten. With no workspace (or a
+ * smaller one) the call takes the row-streaming path instead: same results up to fp32
+ * rounding order, somewhat lower bandwidth. The tiled path launches cooperatively (every
+ * workgroup resident); if the device refuses that, the call streams rows.
+ *
  * Reference interface replaced (saeeddhqan/fpscan):
  *   csrc/main.cpp:7-11              PYBIND11_MODULE: "fullscan_forward" -> warpscan_fwd
  *   csrc/full_scan/full_scan.h:26-36 warpscan_fwd(Ax, Bx, out, reverse)
@@ -80,9 +88,10 @@ int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out,
                     int dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* Device workspace, in bytes, that fpscan_scan_fwd/fpscan_scan_bwd need for this problem
- * (0 when none). No reference counterpart: the reference kernel keeps its carries in
- * shared memory (full_scan.cu:55-57). */
+/* Device workspace, in bytes, that the tiled path of fpscan_scan_fwd/fpscan_scan_bwd uses
+ * for this problem; 0 when the problem takes the row-streaming path (which needs none).
+ * No reference counterpart: the reference kernel keeps its carries in shared memory
+ * (full_scan.cu:55-57). */
 size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype, int op);
 
 /* Static description of a status code (never NULL). The reference's equivalent is the
@@ -99,6 +108,12 @@ int fpscan_abi_version(void);
  * depth never changes results. No reference counterpart: the
  * reference fixes its tiles at compile time (full_scan.cu:207-233). */
 int fpscan_set_launch_override(int waves_per_row, int ring_depth);
+
+/* Path selection for tests and tuning; process-wide. 0: automatic (tiled for problems of at
+ * least 512 MiB per tensor when a workspace is given, except the fp32 forward/reverse scan,
+ * which streams rows), 1: row streaming only, 2: tiled
+ * whenever the row has 16..1024 sub-chunks and a workspace is given. No reference counterpart. */
+int fpscan_set_tiling(int mode);
 
 #ifdef __cplusplus
 }

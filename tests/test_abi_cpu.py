@@ -53,7 +53,7 @@ def lib():
 def test_header_declares_the_expected_entry_points():
     names = header_functions()
     assert {"fpscan_scan_fwd", "fpscan_scan_bwd", "fpscan_workspace_bytes", "fpscan_strerror",
-            "fpscan_abi_version", "fpscan_set_launch_override"} <= set(names)
+            "fpscan_abi_version", "fpscan_set_launch_override", "fpscan_set_tiling"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -74,10 +74,30 @@ def test_strerror_covers_every_status(lib):
     assert "power of 2" in lib.fpscan_strerror(d["FPSCAN_ERR_SEQLEN"]).decode()
 
 
-def test_workspace_is_zero(lib):
-    # the row-streaming kernels keep every carry in registers / LDS
-    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) == 0
-    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 1) == 0
+def test_workspace_plan(lib):
+    lib.fpscan_set_tiling.argtypes = [ctypes.c_int]
+    # tiled path: one 8-byte status word per tile of 16 sub-chunks, plus an overrun counter
+    tiles_bf16 = 8 * 1024 * (65536 // 512 // 16)
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) == 8 * (tiles_bf16 + 1)
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 1) == 8 * (tiles_bf16 + 1)
+    tiles_f32 = 8 * 1024 * (65536 // 256 // 16)
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 0, 1) == 8 * (tiles_f32 + 1)
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 0, 0) == 0  # fp32 forward streams rows
+    # small problems and short rows stream rows and need nothing
+    assert lib.fpscan_workspace_bytes(2, 256, 1024, 0, 0) == 0
+    assert lib.fpscan_workspace_bytes(64, 4096, 256, 0, 0) == 0
+    assert lib.fpscan_workspace_bytes(2, 256, 65536, 0, 0) == 0  # 128 MiB per tensor
+    assert lib.fpscan_workspace_bytes(0, 4, 65536, 2, 0) == 0
+    assert lib.fpscan_workspace_bytes(2, 4, 100, 2, 0) == 0
+    try:
+        assert lib.fpscan_set_tiling(1) == 0  # row streaming only
+        assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) == 0
+        assert lib.fpscan_set_tiling(2) == 0  # tiled whenever the row allows
+        assert lib.fpscan_workspace_bytes(1, 2, 8192, 2, 0) == 8 * (2 * 1 + 1)
+        assert lib.fpscan_workspace_bytes(1, 2, 4096, 2, 0) == 0  # < 16 sub-chunks per row
+        assert lib.fpscan_set_tiling(3) != 0
+    finally:
+        lib.fpscan_set_tiling(0)
 
 
 FAKE = 0x10000  # 16-byte aligned, never dereferenced: every call below fails validation

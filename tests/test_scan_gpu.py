@@ -410,3 +410,115 @@ def test_config5_b64_d4096_l256_and_transposed_layout():
     gg_ref, gx_ref = oracle.scan_bwd_f64(g, out, go)
     check(gx, gx_ref, torch.float32, "c5 grad_tokens")
     check(gg, gg_ref, torch.float32, "c5 grad_gates")
+
+
+# ------------------------------------------------------------------ tiled path (persistent
+# grid, decoupled look-back), called through the C ABI so the workspace can be inspected
+def _abi():
+    import ctypes
+    import os
+
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(fpscan_amd.__file__), "libfpscan_hip.so"))
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_scan_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                    ctypes.c_int, vp, ctypes.c_size_t, vp]
+    lib.fpscan_scan_bwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                    vp, ctypes.c_size_t, vp]
+    lib.fpscan_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int, ctypes.c_int]
+    lib.fpscan_workspace_bytes.restype = ctypes.c_size_t
+    lib.fpscan_set_tiling.argtypes = [ctypes.c_int]
+    return lib
+
+
+_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+
+def _abi_scan(lib, g, x, reverse, tiled):
+    B, D, L = x.shape
+    out = torch.empty_like(x)
+    nbytes = lib.fpscan_workspace_bytes(B, D, L, _CODE[x.dtype], 0) if tiled else 0
+    ws = torch.zeros(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
+    st = lib.fpscan_scan_fwd(g.data_ptr(), x.data_ptr(), out.data_ptr(), B, D, L, D * L, L,
+                             _CODE[x.dtype], int(reverse), ws.data_ptr() if nbytes else None,
+                             nbytes, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    return out, ws, nbytes
+
+
+def _abi_bwd(lib, g, y, go, tiled):
+    B, D, L = g.shape
+    gg, gx = torch.empty_like(g), torch.empty_like(g)
+    nbytes = lib.fpscan_workspace_bytes(B, D, L, _CODE[g.dtype], 1) if tiled else 0
+    ws = torch.zeros(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
+    st = lib.fpscan_scan_bwd(g.data_ptr(), y.data_ptr(), go.data_ptr(), gg.data_ptr(),
+                             gx.data_ptr(), B, D, L, D * L, L, _CODE[g.dtype],
+                             ws.data_ptr() if nbytes else None, nbytes,
+                             torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    return gg, gx, ws, nbytes
+
+
+def _overruns(ws, nbytes):
+    """The last status word counts look-back waits that hit their bound: 0 in a good run."""
+    return int(ws[nbytes - 8:nbytes].view(torch.int64).item())
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("shape", [(1, 3, 8192), (2, 8, 16384), (3, 5, 65536), (32, 64, 8192)])
+def test_tiled_path_matches_oracle(dtype, shape):
+    """Shapes from one tile per row (fp16/bf16 at 8192) to 64 tiles per row (fp32 at 65536)."""
+    lib = _abi()
+    lib.fpscan_set_tiling(2)
+    try:
+        g, x = make_inputs(*shape, dtype, seed=sum(shape))
+        gd, xd = g.to(DEVICE), x.to(DEVICE)
+        for rev in (False, True):
+            out, ws, nbytes = _abi_scan(lib, gd, xd, rev, tiled=True)
+            assert nbytes > 0
+            torch.cuda.synchronize()
+            assert _overruns(ws, nbytes) == 0
+            check(out, oracle.scan_f64(g, x, rev), dtype, f"tiled rev={rev}")
+        go = torch.randn(g.shape, generator=torch.Generator().manual_seed(8)).to(dtype)
+        y = fpscan_amd.scan_forward(gd, xd)
+        gg, gx, ws, nbytes = _abi_bwd(lib, gd, y, go.to(DEVICE), tiled=True)
+        torch.cuda.synchronize()
+        assert _overruns(ws, nbytes) == 0
+        gg_ref, gx_ref = oracle.scan_bwd_f64(g, y.cpu(), go)
+        check(gx, gx_ref, dtype, "tiled grad_tokens")
+        check(gg, gg_ref, dtype, "tiled grad_gates")
+    finally:
+        lib.fpscan_set_tiling(0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_tiled_path_exact_on_integer_data(dtype):
+    lib = _abi()
+    lib.fpscan_set_tiling(2)
+    try:
+        gen = torch.Generator().manual_seed(99)
+        L = 65536
+        gi = (torch.randint(0, 16, (2, 3, L), generator=gen) > 0).to(dtype)
+        xi = torch.randint(-3, 4, (2, 3, L), generator=gen).to(dtype)
+        for rev in (False, True):
+            out, ws, nbytes = _abi_scan(lib, gi.to(DEVICE), xi.to(DEVICE), rev, tiled=True)
+            want = torch.from_numpy(oracle.scan_f64(gi, xi, rev))
+            if dtype == torch.float32 or want.abs().max() < 256:
+                assert bits_equal(out.cpu(), want.to(dtype))
+            assert _overruns(ws, nbytes) == 0
+    finally:
+        lib.fpscan_set_tiling(0)
+
+
+def test_tiled_and_streaming_paths_agree_and_default_is_tiled_when_large():
+    lib = _abi()
+    g, x, go = _bench_inputs(8, 1024, 65536, torch.bfloat16, "mamba", seed=6)  # 1 GiB each
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) > 0  # tiled by default at this size
+    assert lib.fpscan_workspace_bytes(2, 512, 65536, 2, 0) == 0  # 64 MiB: rows are streamed
+    tiled, ws, nbytes = _abi_scan(lib, g, x, False, tiled=True)
+    streamed, _, _ = _abi_scan(lib, g, x, False, tiled=False)
+    torch.cuda.synchronize()
+    assert _overruns(ws, nbytes) == 0
+    assert oracle.normwise_error(tiled, streamed) < 2e-2
+    rows = torch.linspace(0, 8191, 16).long()
+    gs, xs = g.reshape(8192, -1)[rows].cpu(), x.reshape(8192, -1)[rows].cpu()
+    check(tiled.reshape(8192, -1)[rows], oracle.scan_f64(gs, xs), torch.bfloat16, "tiled c4")
