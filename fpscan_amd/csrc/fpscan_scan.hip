@@ -494,12 +494,13 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
 }
 
 // ---------------------------------------------------------------------------------------
-// Long rows, tiled: a persistent, co-resident grid walks tiles in memory order.
+// Long rows, tiled: a persistent grid walks tiles in memory order.
 //
 // A tile is TW consecutive sub-chunks of one row (TW KiB of each tensor), handled by one
-// workgroup of TW waves; workgroup b takes tiles b, b + G, b + 2G, ... (G = grid size), so
-// the tiles in flight at any moment form one contiguous window of each tensor -- the access
-// pattern of a plain streaming kernel. Tiles of one row are chained by a decoupled look-back:
+// workgroup of TW waves. Workgroups claim tiles in increasing order from counters (one atomic
+// per tile; see Claims), so the tiles in flight at any moment form a few contiguous windows
+// of each tensor -- the access pattern of a plain streaming kernel. Tiles of one row are
+// chained by a decoupled look-back:
 //   1. each tile reduces its own data to one affine map (A, B) and publishes it at once as
 //      one 64-bit word in `status` (B in the high half, A in the low half; all-ones = not yet
 //      published; NaNs are canonicalised so all-ones never occurs as data);
@@ -512,11 +513,15 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
 // issuing the next operand loads, since vector loads complete in issue order); the workgroup
 // then reduces tile k+1 and only after that uses the words to finish tile k. A ring of three
 // tiles per workgroup (k finishing, k+1 reducing, k+2 in flight) holds the operands.
-// Publishing never waits, so the dependencies are acyclic: with every workgroup resident
-// (cooperative launch), the workgroup owning the lowest unpublished tile only ever waits on
-// lower tiles, which are published, and makes progress. Each wait is also bounded; a wait
-// that exceeds the bound (which a correct launch never reaches) bumps the overrun word after
-// the status array and proceeds, so the kernel always terminates.
+// Forward progress needs no co-residency: publishing never waits, a tile is claimed only by a
+// workgroup that is already running, and a tile's predecessors were claimed before it. So,
+// within each claim group, the workgroup owning the lowest unpublished tile is running and
+// only ever waits on lower tiles, which are published; it makes progress. Each wait is also
+// bounded; a wait that exceeds the bound (which a correct launch never reaches) bumps the
+// overrun word after the status array and proceeds, so the kernel always terminates.
+//
+// Workspace layout (8-byte words): [0, ntiles) tile status, [ntiles] wait overruns,
+// [ntiles + kCounterStride * (1 + g)] claim counter of group g.
 // ---------------------------------------------------------------------------------------
 constexpr uint64_t kNotPublished = ~0ull;
 constexpr int kSpinLimit = 1 << 16;  // polls of ~1 us each (a device-coherent load)
@@ -529,10 +534,90 @@ __device__ __forceinline__ uint64_t pack_map(float A, float B) {
   return ((uint64_t)canonical_bits(B) << 32) | canonical_bits(A);
 }
 
-__global__ void __launch_bounds__(256) clear_status(uint64_t* __restrict__ status, int64_t n) {
+constexpr int kClaimGroups = 8;
+constexpr int kCounterStride = 16;  // words: each counter on its own 128-byte line
+constexpr int kStatusExtraWords = kCounterStride * (1 + kClaimGroups);
+
+__global__ void __launch_bounds__(256) clear_status(uint64_t* __restrict__ status, int64_t ntiles) {
+  const int64_t n = ntiles + kStatusExtraWords;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-    status[i] = (i == n - 1) ? 0ull : kNotPublished;  // the last word counts wait overruns
+    status[i] = (i < ntiles) ? kNotPublished : 0ull;
 }
+
+// Tile claims, made by one lane per workgroup. One counter at one address serialises at the
+// memory side (measured: about 70 claims per microsecond, fewer than a bf16 forward scan
+// finishes tiles), so the rows are split into kClaimGroups contiguous ranges with a counter
+// each. A workgroup starts in group blockIdx % kClaimGroups (its XCD under round-robin
+// dispatch) and, when that one is used up, moves to the group with the most tiles left. A
+// row never spans two groups and tiles of a group are claimed in order, so a tile's
+// predecessors are always claimed before it. Claims are issued two steps before their tile
+// is needed (an atomic at the memory side takes a few microseconds under full streaming
+// load), so each claim is kept with the group it was made in. In the main loop every lane of every wave issues the claim as a
+// buffer atomic that is out of range except in the leader's lane: a claim inside a branch, or
+// any use of its result before it is resolved, makes the compiler wait for it together with
+// every load issued before it. Counters are the low 32 bits of their words.
+struct Claim {
+  uint32_t raw;
+  int grp;
+};
+
+struct Claims {
+  uint32_t counters_off;  // byte offset of group 0's counter in the status buffer
+  const uint32_t* counters;
+  int64_t rows;
+  int tpr_log2;
+  int grp;
+
+  __device__ int64_t group_first(int g) const {
+    return ((int64_t)g * rows / kClaimGroups) << tpr_log2;
+  }
+  __device__ uint32_t counter_off() const {
+    return counters_off + (uint32_t)(grp * kCounterStride * sizeof(uint64_t));
+  }
+  // Straight-line claim: `mine` selects the one lane that really claims.
+  __device__ Claim issue(Rsrc st, bool mine) const {
+    return Claim{(uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
+                     1, st, mine ? counter_off() : kNoOffset, 0, 0),
+                 grp};
+  }
+  // The group with the most unclaimed tiles, or -1 when every tile is claimed. All counters
+  // are read at once (one round trip).
+  __device__ int pick_group() const {
+    uint32_t c[kClaimGroups];
+#pragma unroll
+    for (int g = 0; g < kClaimGroups; ++g)
+      c[g] = __hip_atomic_load(counters + 2 * kCounterStride * g, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    int best = -1;
+    int64_t best_left = 0;
+#pragma unroll
+    for (int g = 0; g < kClaimGroups; ++g) {
+      const int64_t left = group_first(g + 1) - group_first(g) - (int64_t)c[g];
+      if (left > best_left) {
+        best_left = left;
+        best = g;
+      }
+    }
+    return best;
+  }
+  // The tile a claim stands for: a tile index, `bubble` when its group was used up (claims
+  // then go to the group with the most tiles left), or `done` once every tile is claimed.
+  __device__ int64_t resolve(Claim c, int64_t bubble, int64_t done) {
+    const int64_t lo = group_first(c.grp);
+    if (lo + (int64_t)c.raw < group_first(c.grp + 1)) return lo + (int64_t)c.raw;
+    if (c.grp != grp) return bubble;  // made before the move to the current group
+    const int g = pick_group();
+    if (g < 0) return done;
+    grp = g;
+    return bubble;
+  }
+  // Claims until a tile or `done` comes back (start-up, leader only: waits for each atomic).
+  __device__ int64_t next_now(Rsrc st, int64_t bubble, int64_t done) {
+    int64_t t = bubble;
+    while (t == bubble) t = resolve(issue(st, true), bubble, done);
+    return t;
+  }
+};
 
 // Per-slot state of the tile ring: the tile, its row resources, its segment in the row and
 // the operands of this wave's sub-chunk.
@@ -609,53 +694,92 @@ __device__ __forceinline__ uint32_t tile_maps(const TileSlot<kMode>& ts, int nsu
   return sb;
 }
 
-template <class E, int kMode, int TW>
+template <class E, int kMode, int TW, int D>
 __global__ void __launch_bounds__(64 * TW)
 scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, const int64_t ntiles) {
   constexpr int V = E::V;
   constexpr int kSub = 64 * V;
   constexpr bool kReverse = kMode != kFwd;
+  // ring slots: the tile being reduced, D reduced tiles waiting for their carry (the oldest is
+  // finished this step) and one tile in flight
+  constexpr int N = D + 2;
+  static_assert(N % D == 0, "the unrolled ring must map each step to a fixed deferral slot");
 
   __shared__ f32x2 exch[TW];
   __shared__ float tile_carry;
+  __shared__ int64_t claimed;
+  __shared__ int64_t first_tiles[2];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool leader = threadIdx.x == 0;
   const int vec = kReverse ? 63 - lane : lane;
   const uint32_t lane_off = (uint32_t)vec * 16u;
   const int nsub = a.seqlen / kSub;
   const int row_bytes = a.seqlen * E::kSize;
-  const int64_t G = gridDim.x;
-  const Rsrc st = __builtin_amdgcn_make_buffer_rsrc(status, (short)0,
-                                                    (int)((ntiles + 1) * sizeof(uint64_t)),
-                                                    kRsrcWord3);
+  const Rsrc st = __builtin_amdgcn_make_buffer_rsrc(
+      status, (short)0, (int)((ntiles + kStatusExtraWords) * sizeof(uint64_t)), kRsrcWord3);
 
-  TileSlot<kMode> ring[3];
-  tile_setup<E, kMode, TW>(a, ring[0], blockIdx.x, ntiles, tpr_log2, w, lane_off);
-  __builtin_amdgcn_sched_barrier(0);
-  tile_setup<E, kMode, TW>(a, ring[1], blockIdx.x + G, ntiles, tpr_log2, w, lane_off);
-  __builtin_amdgcn_sched_barrier(0);
-  ring[2].tile = ntiles;  // filled with tile b + 2G at the end of the first step
-  ring[2].seg = 0;
-  ring[2].rr = ring[0].rr;
-
-  // what the previous tile's finish needs from its reduce: the lane's inclusive map, the
-  // wave's exclusive prefix inside the tile, and (wave 0) the predecessor words
-  float held_A = 1.0f, held_B = 0.0f, held_pA = 1.0f, held_pB = 0.0f;
-  uint64_t held_word = 0;
-  bool have_prev = false;
-
-  // A fixed trip count (this workgroup's tiles, plus one step that only finishes the last,
-  // rounded up to whole rings; surplus steps touch no memory) instead of an exit inside the
-  // unrolled body: with an exit there, the compiler's wait counts at the loop head collapse to
-  // waiting for every load in flight.
-  const int64_t mine = (ntiles - blockIdx.x + G - 1) / G;
-  const int64_t steps = ((mine + 1 + 2) / 3) * 3;
-  for (int64_t k0 = 0; k0 < steps; k0 += 3) {
+  // Claim results: a tile index, kBubble (no tile this step, more to come) or kDone.
+  const int64_t kBubble = ntiles, kDone = ntiles + 1;
+  Claims claims{(uint32_t)((ntiles + kCounterStride) * sizeof(uint64_t)),
+                reinterpret_cast<const uint32_t*>(status + ntiles + kCounterStride),
+                ntiles >> tpr_log2, tpr_log2, (int)(blockIdx.x % kClaimGroups)};
+  // leader: claims in flight. Step u of the unrolled ring issues into pending[u] and resolves
+  // pending[(u + D) % N], issued two steps earlier; no copies, which would wait for the atomic.
+  Claim pending[N];
 #pragma unroll
-    for (int u = 0; u < 3; ++u) {
+  for (int i = 0; i < N; ++i) pending[i] = Claim{0, 0};
+  bool claims_done = false;
+  if (leader) {
+    const int64_t t0 = claims.next_now(st, kBubble, kDone);
+    const int64_t t1 = (t0 == kDone) ? kDone : claims.next_now(st, kBubble, kDone);
+    first_tiles[0] = t0;
+    first_tiles[1] = t1;
+    claims_done = t1 == kDone;
+  }
+  pending[N - 2] = claims.issue(st, leader && !claims_done);
+  pending[N - 1] = claims.issue(st, leader && !claims_done);
+  __syncthreads();
+  TileSlot<kMode> ring[N];
+  tile_setup<E, kMode, TW>(a, ring[0], min(__builtin_amdgcn_readfirstlane(first_tiles[0]), ntiles),
+                           ntiles, tpr_log2, w, lane_off);
+  __builtin_amdgcn_sched_barrier(0);
+  tile_setup<E, kMode, TW>(a, ring[1], min(__builtin_amdgcn_readfirstlane(first_tiles[1]), ntiles),
+                           ntiles, tpr_log2, w, lane_off);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 2; i < N; ++i) {  // filled at the end of the first steps
+    ring[i].tile = ntiles;
+    ring[i].seg = 0;
+    ring[i].rr = ring[0].rr;
+  }
+
+  // what a deferred tile's finish needs from its reduce: the lane's inclusive map and the
+  // wave's exclusive prefix inside the tile; and (wave 0) the predecessor words of the tile
+  // finished next, loaded one step ahead
+  float held_A[D], held_B[D], held_pA[D], held_pB[D];
+  bool have[D];
+  uint64_t held_word = 0;
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    held_A[i] = 1.0f;
+    held_B[i] = 0.0f;
+    held_pA[i] = 1.0f;
+    held_pB[i] = 0.0f;
+    have[i] = false;
+  }
+  bool all_claimed = false;  // uniform: the leader has no more tiles to hand out
+
+  // The exit test sits after whole rings (surplus steps touch no memory): with an exit inside
+  // the unrolled body, the compiler's wait counts at the loop head collapse to waiting for
+  // every load in flight.
+  for (;;) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
       TileSlot<kMode>& cur = ring[u];
-      TileSlot<kMode>& prev = ring[(u + 2) % 3];
+      TileSlot<kMode>& fin = ring[(u + 2) % N];  // reduced D steps ago
+      const int hs = u % D;  // deferral slot of `fin` (and of `cur` after this step)
       const bool cur_live = cur.tile < ntiles;  // uniform across the workgroup
 
       // (1) reduce the current tile (a dead tile reduces zeros and publishes nothing)
@@ -682,15 +806,15 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
       status_store(st, publisher ? (uint32_t)(cur.tile * sizeof(uint64_t)) : kNoOffset,
                    pack_map(readlane(eA, TW - 1), readlane(eB, TW - 1)));
 
-      // (2) the previous tile's carry from its predecessor words (loaded by wave 0 at the end
-      // of the previous step; other waves hold zeros and compute a carry nobody uses)
+      // (2) the finishing tile's carry from its predecessor words (loaded by wave 0 right
+      // after its reduce; other waves hold zeros and compute a carry nobody uses)
       uint64_t word = held_word;
       if (__builtin_amdgcn_ballot_w64(word == kNotPublished) != 0) {
         // a predecessor was not published yet: poll (bounded). The poll is an atomic load,
         // which the compiler must re-issue every iteration (a plain buffer load would be
         // hoisted out of the loop).
-        const int64_t p = prev.tile - 64 + lane;
-        const bool in_row = p >= prev.tile - prev.seg;
+        const int64_t p = fin.tile - 64 + lane;
+        const bool in_row = p >= fin.tile - fin.seg;
         for (int it = 0;; ++it) {
           __builtin_amdgcn_s_sleep(1);
           word = in_row ? __hip_atomic_load(status + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -709,42 +833,65 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
       float mB = __uint_as_float((uint32_t)(word >> 32));
       wave_scan(mA, mB);
       if (w == 0 && lane == 63) tile_carry = mB;
+      if (leader) {
+        const int64_t t = claims_done ? kDone : claims.resolve(pending[(u + D) % N], kBubble, kDone);
+        claims_done = t == kDone;
+        claimed = t;
+      }
       lds_barrier();
+      const int64_t claim = __builtin_amdgcn_readfirstlane(claimed);
+      all_claimed = claim == kDone;
+      const int64_t refill = claim < ntiles ? claim : ntiles;
 
-      // (3) finish the previous tile (nothing is stored on the first step)
+      // (3) finish the oldest deferred tile (nothing is stored while the ring fills)
       {
         const float c_tile = tile_carry;
-        const float c_in = fmaf(held_pA, c_tile, held_pB);
+        const float c_in = fmaf(held_pA[hs], c_tile, held_pB[hs]);
         float pal[V], pbe[V], pys[V];
-        const uint32_t sb = tile_maps<E, kMode, TW>(prev, nsub, row_bytes, w, lane, pal, pbe, pys);
-        const float y_lane_end = fmaf(held_A, c_in, held_B);
+        const uint32_t sb = tile_maps<E, kMode, TW>(fin, nsub, row_bytes, w, lane, pal, pbe, pys);
+        const float y_lane_end = fmaf(held_A[hs], c_in, held_B[hs]);
         const float y_enter = dpp<kWaveShr1>(c_in, y_lane_end);
         u32x4 o0, o1;
         finish_lane<E, kMode>(pal, pbe, pys, y_enter, o0, o1);
-        const uint32_t so = have_prev ? sb + lane_off : kNoOffset;
-        bst16(prev.rr.out0, so, o0);
-        if constexpr (kMode == kBwd) bst16(prev.rr.out1, so, o1);
+        const uint32_t so = have[hs] ? sb + lane_off : kNoOffset;
+        bst16(fin.rr.out0, so, o0);
+        if constexpr (kMode == kBwd) bst16(fin.rr.out1, so, o1);
       }
-      held_A = A;
-      held_B = B;
-      held_pA = cur_pA;
-      held_pB = cur_pB;
-      have_prev = cur_live;
+      held_A[hs] = A;
+      held_B[hs] = B;
+      held_pA[hs] = cur_pA;
+      held_pB[hs] = cur_pB;
+      have[hs] = cur_live;
 
-      // (4) wave 0: load the current tile's predecessor words now, before the refill below:
-      // vector loads complete in issue order, so waiting for these words in the next step
-      // does not wait for the refill. By then the neighbouring workgroups, which reduce the
-      // predecessors at the same pace, have normally published them. Lanes before the row
-      // start (and all other waves) read 0: the constant map 0, the zero initial state.
+      // (4) wave 0: load the predecessor words of the tile finished in the next step (reduced
+      // D - 1 steps ago, or just now when D = 1) now, before the refill below: vector loads
+      // complete in issue order, so waiting for these words in the next step does not wait
+      // for the refill. Loading as late as that gives the workgroups that claimed the
+      // predecessors, just before that tile was claimed, D steps to publish them. Lanes before
+      // the row start (and all other waves) read 0: the constant map 0, the zero initial
+      // state.
       {
-        const int64_t q = cur.tile - 64 + lane;
-        const bool mine = w == 0 && cur_live && cur.seg > 0 && q >= cur.tile - cur.seg;
+        const TileSlot<kMode>& nxt = ring[(u + 3) % N];
+        const bool nxt_live = nxt.tile < ntiles;
+        const int64_t q = nxt.tile - 64 + lane;
+        const bool mine = w == 0 && nxt_live && nxt.seg > 0 && q >= nxt.tile - nxt.seg;
         held_word = status_load(st, mine ? (uint32_t)(q * sizeof(uint64_t)) : kNoOffset);
       }
-      // (5) refill the finished slot with the tile three steps ahead
-      tile_setup<E, kMode, TW>(a, prev, cur.tile + 2 * G, ntiles, tpr_log2, w, lane_off);
+      // claim the refill two steps ahead now, behind the status words and ahead of the
+      // operand loads, so that its return does not wait for them
+      pending[u] = claims.issue(st, leader && !claims_done);
+      // (5) refill the finished slot with the tile claimed two steps ago
+      tile_setup<E, kMode, TW>(a, fin, refill, ntiles, tpr_log2, w, lane_off);
       __builtin_amdgcn_sched_barrier(0);
     }
+    // done once no claim is left, every slot is past the end and nothing is left to finish
+    // (uniform: the tile indices come from one lane)
+    bool busy = !all_claimed;
+#pragma unroll
+    for (int i = 0; i < D; ++i) busy = busy || have[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) busy = busy || ring[i].tile < ntiles;
+    if (!busy) break;
   }
 }
 
@@ -808,23 +955,25 @@ std::atomic<int> g_tiling{0};  // 0 automatic, 1 row streaming only, 2 tiled whe
 
 // Tiled path geometry: TW sub-chunks per tile, at most 64 tiles per row (one look-back window)
 constexpr int kTileWaves = 16;
-// Below this many bytes per tensor the row-streaming kernels win: the persistent grid needs
-// dozens of tiles per workgroup to amortise filling and draining its three-tile pipeline
-// (measured: fp32 B2 D256 L65536, 128 MiB per tensor, streams at 5.6 TB/s and tiles at 4.4).
+// Steps between a tile's reduce and its finish: a workgroup a step or two behind its
+// neighbours then rarely makes them wait (measured at B8 D1024 L65536: see the kernel notes).
+constexpr int kTileDefer = 2;
+// Below this many bytes per tensor the row-streaming kernels win: a tiled launch costs about
+// 10-15 us more than its streaming time (the status clear, start-up claims, filling and
+// draining the four-tile pipeline), which dozens of tiles per workgroup amortise. Measured on
+// MI355X: at 128 MiB per tensor streaming wins (fp32 B2 D256 L65536 forward 72 us against
+// 87), at 512 MiB tiling wins by 6 % (fp32 B8 D1024 L16384) and at 1-2 GiB by 8-10 %.
 constexpr int64_t kTiledMinBytes = 512ll << 20;
 
 struct TilePlan {
   bool use;
   int tpr;         // tiles per row
   int64_t ntiles;  // rows * tpr
-  size_t bytes;    // workspace: one status word per tile + one overrun counter
+  size_t bytes;    // workspace: one status word per tile + overrun and tile counters
 };
 
-// `backward` selects the plan of fpscan_scan_bwd. In automatic mode the fp32 forward/reverse
-// scan keeps streaming rows: its rows have 16 tiles, so a tile waits on a late predecessor
-// more often (15 % of tiles at B8 D1024 L65536), and the tiled path measured 4 % slower there
-// while every other large case measured 1.5-4.5 % faster.
-TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling, bool backward) {
+// The forward/reverse scan and the backward use the same plan.
+TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling) {
   TilePlan t{false, 0, 0, 0};
   const int64_t sub = 64 * (16 / size);
   const int64_t nsub = seqlen / sub;
@@ -832,11 +981,10 @@ TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling, bool bac
   t.tpr = (int)(nsub / kTileWaves);
   if (t.tpr > 64) return t;
   if (tiling == 0 && rows * seqlen * size < kTiledMinBytes) return t;
-  if (tiling == 0 && size == 4 && !backward) return t;
   t.ntiles = rows * t.tpr;
-  if ((t.ntiles + 1) * (int64_t)sizeof(uint64_t) > INT32_MAX) return t;  // status buffer range
+  if ((t.ntiles + kStatusExtraWords) * (int64_t)sizeof(uint64_t) > INT32_MAX) return t;
   t.use = true;
-  t.bytes = (size_t)(t.ntiles + 1) * sizeof(uint64_t);
+  t.bytes = (size_t)(t.ntiles + kStatusExtraWords) * sizeof(uint64_t);
   return t;
 }
 
@@ -910,19 +1058,21 @@ const void* short_kernel(int g) {
 // Chooses the launch for one problem. Rows are independent; long rows are owned by W waves
 // (W = 16 when the row has at least 16 sub-chunks) with U sub-chunks in flight per wave. The
 // ring depths are the deepest that keep every variant within 64 VGPRs (8 waves per SIMD).
-// Tiled launch: clear the status words, then the persistent grid with every workgroup
-// resident (cooperative launch). Returns -1 when the device refuses the cooperative launch,
-// so that the caller can stream rows instead.
+// Tiled launch: clear the status words and counters, then the persistent grid, one workgroup
+// per resident slot (more would only queue behind them; fewer is also correct, since tiles
+// are claimed dynamically). Returns -1 when the occupancy query fails, so that the caller
+// streams rows instead.
 template <class E, int kMode>
 int run_tiled(const Args& a, const TilePlan& plan, void* workspace, hipStream_t stream, int slot) {
-  const void* kernel = reinterpret_cast<const void*>(&scan_tiles<E, kMode, kTileWaves>);
+  const void* kernel = reinterpret_cast<const void*>(&scan_tiles<E, kMode, kTileWaves, kTileDefer>);
   const int threads = 64 * kTileWaves;
   const int resident = resident_blocks(kernel, slot, threads);
   if (resident <= 0) return -1;
   uint64_t* status = static_cast<uint64_t*>(workspace);
-  const int64_t nwords = plan.ntiles + 1;
+  int64_t ntiles = plan.ntiles;
+  const int64_t nwords = ntiles + kStatusExtraWords;
   const int64_t clear_blocks = (nwords + 255) / 256 < 1024 ? (nwords + 255) / 256 : 1024;
-  void* cargs[] = {&status, const_cast<int64_t*>(&nwords)};
+  void* cargs[] = {&status, &ntiles};
   if (hipLaunchKernel(reinterpret_cast<const void*>(&clear_status), dim3((unsigned)clear_blocks),
                       dim3(256), cargs, 0, stream) != hipSuccess)
     return FPSCAN_ERR_LAUNCH;
@@ -930,13 +1080,10 @@ int run_tiled(const Args& a, const TilePlan& plan, void* workspace, hipStream_t 
   Args copy = a;
   int tpr_log2 = 0;
   while ((1 << tpr_log2) < plan.tpr) ++tpr_log2;
-  int64_t ntiles = plan.ntiles;
   void* kargs[] = {&copy, &status, &tpr_log2, &ntiles};
-  const hipError_t err = hipLaunchCooperativeKernel(kernel, dim3((unsigned)grid), dim3(threads),
-                                                    kargs, 0, stream);
-  if (err == hipSuccess) return FPSCAN_OK;
-  (void)hipGetLastError();  // clear the refusal; the caller streams rows instead
-  return -1;
+  const hipError_t err =
+      hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), kargs, 0, stream);
+  return err == hipSuccess ? FPSCAN_OK : FPSCAN_ERR_LAUNCH;
 }
 
 template <class E, int kMode>
@@ -945,7 +1092,7 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   constexpr int kSub = 64 * V;
   const int L = a.seqlen;
   const TilePlan plan =
-      plan_tiles(a.rows, L, E::kSize, g_tiling.load(std::memory_order_relaxed), kMode == kBwd);
+      plan_tiles(a.rows, L, E::kSize, g_tiling.load(std::memory_order_relaxed));
   if (plan.use && workspace != nullptr && ws_bytes >= plan.bytes) {
     const int st = run_tiled<E, kMode>(a, plan, workspace, stream,
                                        E::kSlot * 3 + kMode);
@@ -1065,8 +1212,9 @@ size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dt
   if (size == 0 || batch <= 0 || dim <= 0 || seqlen < 32 || seqlen > 65536 ||
       (seqlen & (seqlen - 1)) != 0)
     return 0;
+  if (op != FPSCAN_OP_FWD && op != FPSCAN_OP_BWD) return 0;
   const TilePlan plan = plan_tiles(batch * dim, seqlen, size,
-                                   g_tiling.load(std::memory_order_relaxed), op == FPSCAN_OP_BWD);
+                                   g_tiling.load(std::memory_order_relaxed));
   return plan.use ? plan.bytes : 0;
 }
 

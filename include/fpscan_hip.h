@@ -17,12 +17,13 @@
  * aligned and the strides must be multiples of 16 bytes (16/itemsize elements).
  *
  * Workspace: large problems run fastest on the tiled path, which needs
- * fpscan_workspace_bytes() bytes of device memory (one 8-byte word per tile, about 0.2 % of
- * one tensor). Pass a buffer of at least that size, 8-byte aligned, owned by the caller and
- * not used by any other call in flight. Its contents are overwritten. With no workspace (or a
- * smaller one) the call takes the row-streaming path instead: same results up to fp32
- * rounding order, somewhat lower bandwidth. The tiled path launches cooperatively (every
- * workgroup resident); if the device refuses that, the call streams rows.
+ * fpscan_workspace_bytes() bytes of device memory (one 8-byte word per tile plus 1152 bytes
+ * of counters, about 0.05 % of one tensor). Pass a buffer of at least that size, 8-byte aligned, owned by the
+ * caller and not used by any other call in flight. Its contents are overwritten. With no
+ * workspace (or a smaller one) the call takes the row-streaming path instead: same results up
+ * to fp32 rounding order, somewhat lower bandwidth. The tiled path is an ordinary launch that
+ * needs no co-residency (workgroups claim tiles in order); if the occupancy query fails, the
+ * call streams rows.
  *
  * Reference interface replaced (saeeddhqan/fpscan):
  *   csrc/main.cpp:7-11              PYBIND11_MODULE: "fullscan_forward" -> warpscan_fwd
@@ -110,8 +111,7 @@ int fpscan_abi_version(void);
 int fpscan_set_launch_override(int waves_per_row, int ring_depth);
 
 /* Path selection for tests and tuning; process-wide. 0: automatic (tiled for problems of at
- * least 512 MiB per tensor when a workspace is given, except the fp32 forward/reverse scan,
- * which streams rows), 1: row streaming only, 2: tiled
+ * least 512 MiB per tensor when a workspace is given), 1: row streaming only, 2: tiled
  * whenever the row has 16..1024 sub-chunks and a workspace is given. No reference counterpart. */
 int fpscan_set_tiling(int mode);
 

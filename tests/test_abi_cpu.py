@@ -76,13 +76,15 @@ def test_strerror_covers_every_status(lib):
 
 def test_workspace_plan(lib):
     lib.fpscan_set_tiling.argtypes = [ctypes.c_int]
-    # tiled path: one 8-byte status word per tile of 16 sub-chunks, plus an overrun counter
+    # tiled path: one 8-byte status word per tile of 16 sub-chunks, then an overrun counter
+    # and 8 claim counters, each on its own 128-byte line
+    extra = 16 * (1 + 8)
     tiles_bf16 = 8 * 1024 * (65536 // 512 // 16)
-    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) == 8 * (tiles_bf16 + 1)
-    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 1) == 8 * (tiles_bf16 + 1)
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) == 8 * (tiles_bf16 + extra)
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 1) == 8 * (tiles_bf16 + extra)
     tiles_f32 = 8 * 1024 * (65536 // 256 // 16)
-    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 0, 1) == 8 * (tiles_f32 + 1)
-    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 0, 0) == 0  # fp32 forward streams rows
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 0, 1) == 8 * (tiles_f32 + extra)
+    assert lib.fpscan_workspace_bytes(8, 1024, 65536, 0, 0) == 8 * (tiles_f32 + extra)
     # small problems and short rows stream rows and need nothing
     assert lib.fpscan_workspace_bytes(2, 256, 1024, 0, 0) == 0
     assert lib.fpscan_workspace_bytes(64, 4096, 256, 0, 0) == 0
@@ -93,7 +95,7 @@ def test_workspace_plan(lib):
         assert lib.fpscan_set_tiling(1) == 0  # row streaming only
         assert lib.fpscan_workspace_bytes(8, 1024, 65536, 2, 0) == 0
         assert lib.fpscan_set_tiling(2) == 0  # tiled whenever the row allows
-        assert lib.fpscan_workspace_bytes(1, 2, 8192, 2, 0) == 8 * (2 * 1 + 1)
+        assert lib.fpscan_workspace_bytes(1, 2, 8192, 2, 0) == 8 * (2 * 1 + extra)
         assert lib.fpscan_workspace_bytes(1, 2, 4096, 2, 0) == 0  # < 16 sub-chunks per row
         assert lib.fpscan_set_tiling(3) != 0
     finally:

@@ -437,7 +437,7 @@ def _abi_scan(lib, g, x, reverse, tiled):
     B, D, L = x.shape
     out = torch.empty_like(x)
     nbytes = lib.fpscan_workspace_bytes(B, D, L, _CODE[x.dtype], 0) if tiled else 0
-    ws = torch.zeros(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
+    ws = torch.full((max(nbytes, 8),), 0xA5, dtype=torch.uint8, device=DEVICE)  # stale data
     st = lib.fpscan_scan_fwd(g.data_ptr(), x.data_ptr(), out.data_ptr(), B, D, L, D * L, L,
                              _CODE[x.dtype], int(reverse), ws.data_ptr() if nbytes else None,
                              nbytes, torch.cuda.current_stream().cuda_stream)
@@ -449,7 +449,7 @@ def _abi_bwd(lib, g, y, go, tiled):
     B, D, L = g.shape
     gg, gx = torch.empty_like(g), torch.empty_like(g)
     nbytes = lib.fpscan_workspace_bytes(B, D, L, _CODE[g.dtype], 1) if tiled else 0
-    ws = torch.zeros(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
+    ws = torch.full((max(nbytes, 8),), 0xA5, dtype=torch.uint8, device=DEVICE)  # stale data
     st = lib.fpscan_scan_bwd(g.data_ptr(), y.data_ptr(), go.data_ptr(), gg.data_ptr(),
                              gx.data_ptr(), B, D, L, D * L, L, _CODE[g.dtype],
                              ws.data_ptr() if nbytes else None, nbytes,
@@ -458,9 +458,20 @@ def _abi_bwd(lib, g, y, go, tiled):
     return gg, gx, ws, nbytes
 
 
+CLAIM_GROUPS, COUNTER_STRIDE = 8, 16  # workspace tail: overrun word, then 8 claim counters
+
+
 def _overruns(ws, nbytes):
-    """The last status word counts look-back waits that hit their bound: 0 in a good run."""
-    return int(ws[nbytes - 8:nbytes].view(torch.int64).item())
+    """The word after the tile status words counts look-back waits that hit their bound (0 in
+    a good run). Every tile must have been published, and the claim counters must have handed
+    out at least every tile."""
+    words = ws[:nbytes].view(torch.int64)
+    ntiles = nbytes // 8 - COUNTER_STRIDE * (1 + CLAIM_GROUPS)
+    counters = words[ntiles + COUNTER_STRIDE::COUNTER_STRIDE]
+    assert counters.numel() == CLAIM_GROUPS
+    assert int(counters.sum().item()) >= ntiles, "not every tile was claimed"
+    assert (words[:ntiles] != -1).all(), "a tile was never published"
+    return int(words[ntiles].item())
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
