@@ -328,12 +328,49 @@ def bench_shape(args):
     return res
 
 
+def bench_channel_last(args):
+    """c4cl / c5cl: configs 4 and 5 with (batch, seqlen, dim) tensors. Times the channel-last
+    kernels (fwd, rev, fused bwd) and, for comparison, the reference's recipe for this layout:
+    transpose in, row-major scan, transpose out (README.md:94-99)."""
+    import fpscan_amd
+
+    B, D, L, dname, dist = WORKLOADS[args.workload[:2]]
+    dtype = DTYPES[args.dtype or dname]
+    s = torch.empty((), dtype=dtype).element_size()
+    N = B * D * L
+    gr, xr, gor = make_inputs(B, D, L, dtype, dist, seed=1)
+    g, x, go = (t.mT.contiguous() for t in (gr, xr, gor))  # (batch, seqlen, dim)
+    del gr, xr, gor
+    out = torch.empty_like(x)
+    y = fpscan_amd.scan_forward_channel_last(g, x)
+    gg, gx = torch.empty_like(g), torch.empty_like(g)
+    entry = {"workload": args.workload, "shape_bld": [B, L, D], "dtype": SHORT[dtype]}
+    for name, fn, nbytes in (
+        ("fwd", lambda: fpscan_amd.scan_forward_channel_last(g, x, False, out), 3 * N * s),
+        ("rev", lambda: fpscan_amd.scan_forward_channel_last(g, x, True, out), 3 * N * s),
+        ("bwd", lambda: fpscan_amd.scan_backward_channel_last(g, y, go, gg, gx), 5 * N * s),
+    ):
+        t = time_each(fn, 5, args.iters)
+        p50 = percentile(t, 0.5)
+        entry[name] = {"p50_ms": round(p50, 5), "gbps": round(nbytes / (p50 / 1e3) / 1e9, 1)}
+
+    def via_transpose():
+        return fpscan_amd.scan_forward(g.mT.contiguous(), x.mT.contiguous()).mT.contiguous()
+
+    t = time_each(via_transpose, 3, args.iters)
+    p50 = percentile(t, 0.5)
+    entry["fwd_via_transpose"] = {"p50_ms": round(p50, 5),
+                                  "gbps": round(3 * N * s / (p50 / 1e3) / 1e9, 1)}
+    print(json.dumps(entry), flush=True)
+    return entry
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl"])
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -370,6 +407,8 @@ def main():
         res = bench_headline(args)
     elif args.workload == "c2":
         res = bench_sweep(args)
+    elif args.workload.endswith("cl"):
+        res = bench_channel_last(args)
     else:
         res = bench_shape(args)
     print(json.dumps(res), flush=True)

@@ -1,9 +1,13 @@
 """MI355X-native first-order linear-recurrence scan (drop-in for saeeddhqan/fpscan).
 
 Same public names as fpscan/__init__.py:1-3 (``pscan``, ``scan_forward``, ``PScan``), plus
-``scan_backward`` (the fused backward, exposed directly).
+``scan_backward`` (the fused backward, exposed directly) and the channel-last variants for
+(batch, seqlen, dim) tensors (``pscan_channel_last``, ``scan_forward_channel_last``,
+``scan_backward_channel_last``, ``PScanChannelLast``).
 """
-from .ops import PScan, pscan, scan_backward, scan_forward
+from .ops import (PScan, PScanChannelLast, pscan, pscan_channel_last, scan_backward,
+                  scan_backward_channel_last, scan_forward, scan_forward_channel_last)
 
-__all__ = ["pscan", "scan_forward", "scan_backward", "PScan"]
-__version__ = "0.1.2"
+__all__ = ["pscan", "scan_forward", "scan_backward", "PScan", "pscan_channel_last",
+           "scan_forward_channel_last", "scan_backward_channel_last", "PScanChannelLast"]
+__version__ = "0.2.0"

@@ -53,10 +53,14 @@ def _atomic_out(path):
     return path + ".tmp%d" % os.getpid()
 
 
+HIP_SOURCES = ("fpscan_scan.hip", "fpscan_scan_cl.hip")
+
+
 def build_hip_library() -> str:
-    src = os.path.join(CSRC, "fpscan_scan.hip")
+    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
     tmp = _atomic_out(HIP_LIB)
-    _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE_DIR, src, "-o", tmp], "hipcc fpscan_scan.hip")
+    _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE_DIR, "-I", CSRC, *srcs, "-o", tmp],
+         "hipcc " + " ".join(HIP_SOURCES))
     os.replace(tmp, HIP_LIB)
     return HIP_LIB
 

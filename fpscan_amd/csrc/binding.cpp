@@ -7,7 +7,8 @@
 //   csrc/full_scan/full_scan.cu:179-258  stride/dtype checks, tile table, launch on the
 //                                current stream
 // Added: `fullscan_backward`, the fused backward that replaces the composition in
-// fpscan/ops.py:69-83, plus the checks the reference leaves out (shapes, `out`, device).
+// fpscan/ops.py:69-83, plus the checks the reference leaves out (shapes, `out`, device);
+// `fullscan_forward_cl` / `fullscan_backward_cl` for (batch, seqlen, dim) tensors.
 // Every check runs before any HIP call, so a bad call raises RuntimeError on any machine.
 #include <torch/extension.h>
 
@@ -135,6 +136,83 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward(const at::Tensor& gates,
   return {grad_gates, grad_tokens};
 }
 
+// ---- channel-last (batch, seqlen, dim): no reference counterpart (README.md:94-99 has
+// callers transpose instead)
+void check_input_cl(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.device().is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  const auto st = t.scalar_type();
+  TORCH_CHECK(st == at::kHalf || st == at::kBFloat16 || st == at::kFloat, name,
+              " must be float16 or bfloat16 or float32");
+  TORCH_CHECK(t.dim() == 3, name, " must be a 3-d (batch, seqlen, dim) tensor, got ", t.dim(),
+              " dims");
+  const int64_t vec = 16 / (int64_t)t.element_size();
+  TORCH_CHECK(t.size(2) % vec == 0, name, ": dim must be a multiple of ", vec, " for ",
+              t.scalar_type(), " (16-byte vectors), got ", t.size(2));
+}
+
+at::Tensor fullscan_forward_cl(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tensor& out,
+                               bool reverse) {
+  check_input_cl(Ax, "Ax");
+  check_input_cl(Bx, "Bx");
+  check_like(Ax, Bx, "Ax", "Bx");
+  check_input_cl(out, "out");
+  check_like(out, Bx, "out", "Bx");
+  if (Bx.numel() == 0) return out;
+
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
+  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(Bx.device().index()).stream();
+  const int64_t B = Bx.size(0), L = Bx.size(1), D = Bx.size(2);
+  const int dt = dtype_code(Bx.scalar_type());
+  const size_t ws_bytes = fpscan_workspace_bytes_cl(B, L, D, D, dt, FPSCAN_OP_FWD);
+  at::Tensor ws = workspace(ws_bytes, Bx);
+  const int status = fpscan_scan_fwd_cl(Ax.data_ptr(), Bx.data_ptr(), out.data_ptr(), B, L, D,
+                                        L * D, D, dt, reverse ? 1 : 0,
+                                        ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
+  check_status(status);
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor> fullscan_backward_cl(const at::Tensor& gates,
+                                                        const at::Tensor& out,
+                                                        const at::Tensor& grad_out,
+                                                        const at::Tensor& grad_gates,
+                                                        const at::Tensor& grad_tokens) {
+  check_input_cl(gates, "gates");
+  check_input_cl(out, "out");
+  check_input_cl(grad_out, "grad_out");
+  check_input_cl(grad_gates, "grad_gates");
+  check_input_cl(grad_tokens, "grad_tokens");
+  check_like(out, gates, "out", "gates");
+  check_like(grad_out, gates, "grad_out", "gates");
+  check_like(grad_gates, gates, "grad_gates", "gates");
+  check_like(grad_tokens, gates, "grad_tokens", "gates");
+  if (gates.numel() == 0) return {grad_gates, grad_tokens};
+  // neighbouring time steps are read (gates[t+1], out[t-1]) while other waves write
+  for (const at::Tensor* o : {&grad_gates, &grad_tokens}) {
+    for (const at::Tensor* i : {&gates, &out, &grad_out}) {
+      TORCH_CHECK(o->data_ptr() != i->data_ptr(), "fullscan_backward_cl outputs must not "
+                  "alias its inputs");
+    }
+  }
+  TORCH_CHECK(grad_gates.data_ptr() != grad_tokens.data_ptr(),
+              "grad_gates and grad_tokens must be distinct");
+
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(gates.device());
+  void* stream =
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(gates.device().index()).stream();
+  const int64_t B = gates.size(0), L = gates.size(1), D = gates.size(2);
+  const int dt = dtype_code(gates.scalar_type());
+  const size_t ws_bytes = fpscan_workspace_bytes_cl(B, L, D, D, dt, FPSCAN_OP_BWD);
+  at::Tensor ws = workspace(ws_bytes, gates);
+  const int status = fpscan_scan_bwd_cl(gates.data_ptr(), out.data_ptr(), grad_out.data_ptr(),
+                                        grad_gates.data_ptr(), grad_tokens.data_ptr(), B, L, D,
+                                        L * D, D, dt, ws_bytes ? ws.data_ptr() : nullptr,
+                                        ws_bytes, stream);
+  check_status(status);
+  return {grad_gates, grad_tokens};
+}
+
 int set_launch_override(int waves_per_row, int ring_depth) {
   const int status = fpscan_set_launch_override(waves_per_row, ring_depth);
   TORCH_CHECK(status == FPSCAN_OK, "waves_per_row must be one of 0,1,2,4,8,16 and ring_depth "
@@ -150,6 +228,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("Ax"), pybind11::arg("Bx"), pybind11::arg("out"), pybind11::arg("reverse"));
   m.def("fullscan_backward", &fullscan_backward,
         "fused backward of the forward scan: (grad_gates, grad_tokens) (HIP, gfx950)",
+        pybind11::arg("gates"), pybind11::arg("out"), pybind11::arg("grad_out"),
+        pybind11::arg("grad_gates"), pybind11::arg("grad_tokens"));
+  m.def("fullscan_forward_cl", &fullscan_forward_cl,
+        "channel-last scan of (batch, seqlen, dim) tensors along seqlen, written into out",
+        pybind11::arg("Ax"), pybind11::arg("Bx"), pybind11::arg("out"), pybind11::arg("reverse"));
+  m.def("fullscan_backward_cl", &fullscan_backward_cl,
+        "fused backward of the channel-last forward scan: (grad_gates, grad_tokens)",
         pybind11::arg("gates"), pybind11::arg("out"), pybind11::arg("grad_out"),
         pybind11::arg("grad_gates"), pybind11::arg("grad_tokens"));
   m.def("set_launch_override", &set_launch_override,

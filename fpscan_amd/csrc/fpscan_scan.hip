@@ -34,92 +34,9 @@
 #include <atomic>
 
 #include "fpscan_hip.h"
+#include "scan_common.h"
 
 namespace {
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// ---------------------------------------------------------------------------------------
-// Element types: V elements per 16-byte vector, exact widening, round-to-nearest-even
-// narrowing (the reference's to_float/from_float, csrc/full_scan/conversion.h:7-13).
-// ---------------------------------------------------------------------------------------
-struct F32 {
-  static constexpr int V = 4;
-  static constexpr int kSize = 4;
-  static constexpr int kSlot = 0;  // index of this type in per-type tables
-  __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
-  }
-  __device__ static __forceinline__ u32x4 pack(const float (&f)[V]) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __float_as_uint(f[i]);
-    return v;
-  }
-};
-
-struct F16 {
-  static constexpr int V = 8;
-  static constexpr int kSize = 2;
-  static constexpr int kSlot = 1;  // index of this type in per-type tables
-  __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // copy the element out first: a bit_cast of the vector-element lvalue v[i] reads
-      // element 0 for every i with this compiler
-      const unsigned int word = v[i];
-      const f16x2 h = __builtin_bit_cast(f16x2, word);
-      f[2 * i] = static_cast<float>(h.x);
-      f[2 * i + 1] = static_cast<float>(h.y);
-    }
-  }
-  __device__ static __forceinline__ u32x4 pack(const float (&f)[V]) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f16x2 h;
-      h.x = static_cast<_Float16>(f[2 * i]);  // v_cvt_f16_f32: round to nearest even
-      h.y = static_cast<_Float16>(f[2 * i + 1]);
-      v[i] = __builtin_bit_cast(unsigned int, h);
-    }
-    return v;
-  }
-  __device__ static __forceinline__ float widen16(unsigned short bits) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, bits));
-  }
-};
-
-struct BF16 {
-  static constexpr int V = 8;
-  static constexpr int kSize = 2;
-  static constexpr int kSlot = 2;  // index of this type in per-type tables
-  __device__ static __forceinline__ void unpack(const u32x4 v, float (&f)[V]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = __uint_as_float(v[i] << 16);
-      f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
-    }
-  }
-  __device__ static __forceinline__ u32x4 pack(const float (&f)[V]) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x2 x;
-      x.x = f[2 * i];
-      x.y = f[2 * i + 1];
-      // v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN
-      v[i] = __builtin_bit_cast(unsigned int, __builtin_convertvector(x, bf16x2));
-    }
-    return v;
-  }
-  __device__ static __forceinline__ float widen16(unsigned short bits) {
-    return __uint_as_float((unsigned int)bits << 16);
-  }
-};
 
 // ---------------------------------------------------------------------------------------
 // Wave64 lane movement (DPP). Lanes whose source is outside the row / wave, or whose row is
@@ -221,9 +138,6 @@ struct Args {
   int32_t contiguous;
 };
 
-constexpr int kFwd = 0;
-constexpr int kRev = 1;
-constexpr int kBwd = 2;
 
 __device__ __forceinline__ int64_t row_offset(const Args& a, int64_t row) {
   if (a.contiguous) return row * a.seqlen;
@@ -240,28 +154,6 @@ __device__ __forceinline__ void st16(void* base, int64_t elem, int size, u32x4 v
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * size));
 }
 
-// Buffer resources: one per tensor per row, base = the row's first element, range = the
-// row's bytes. Loads and stores then carry only a 32-bit in-row byte offset in a VGPR, and
-// the hardware range check turns any offset outside the row into a zero read / dropped
-// write instead of a fault.
-constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
-constexpr int kCacheNT = 2;             // cache-policy bit: nontemporal (streamed once)
-
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-
-__device__ __forceinline__ Rsrc row_rsrc(const void* p, int64_t row_base, int size, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(static_cast<const char*>(p)) + row_base * size, (short)0, bytes, kRsrcWord3);
-}
-
-// Every element is read once: the 16-byte operand loads are nontemporal, like the stores.
-__device__ __forceinline__ u32x4 bld16(Rsrc r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCacheNT));
-}
-
-__device__ __forceinline__ void bst16(Rsrc r, uint32_t off, u32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCacheNT);
-}
 
 template <class E>
 __device__ __forceinline__ float bld1(Rsrc r, uint32_t off) {
@@ -286,8 +178,6 @@ struct RowRsrc {
   Rsrc in0, in1, in2, out0, out1;
 };
 
-// Byte offset that no row range contains: loads from it return 0 without touching memory.
-constexpr uint32_t kNoOffset = 0x80000000u;
 
 // Issues the loads of one sub-chunk. `sub_bytes` is the wave-uniform byte offset of the
 // sub-chunk inside the row, or kNoOffset for a ring slot past the end of the row (the loads

@@ -20,7 +20,8 @@ from typing import Optional, Tuple
 
 import torch
 
-__all__ = ["pscan", "scan_forward", "scan_backward", "PScan"]
+__all__ = ["pscan", "scan_forward", "scan_backward", "PScan", "pscan_channel_last",
+           "scan_forward_channel_last", "scan_backward_channel_last", "PScanChannelLast"]
 
 _EXT_CANDIDATES = ("fpscan_amd._C",)
 _ext = None
@@ -104,6 +105,68 @@ class PScan(torch.autograd.Function):
 
 def pscan(gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
     return PScan.apply(gates, tokens)
+
+
+# ---------------------------------------------------------------------------------------
+# Channel-last layout: (batch, seqlen, dim), scanned along seqlen. No reference counterpart;
+# the reference's README.md:94-99 transposes in and out around pscan instead, which this
+# path makes unnecessary (same results, no copies).
+# ---------------------------------------------------------------------------------------
+def scan_forward_channel_last(
+    gates: torch.Tensor,
+    tokens: torch.Tensor,
+    reverse: bool = False,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """y[:, t] = gates[:, t]*y[:, t-1] + tokens[:, t] for (batch, seqlen, dim) contiguous
+    fp32/fp16/bf16 tensors (reverse: y[:, t+1]); any seqlen >= 1, dim a multiple of
+    16/itemsize. Equal to ``scan_forward(g.mT.contiguous(), x.mT.contiguous()).mT`` up to fp32
+    rounding order."""
+    ext = _load_extension()
+    if out is None:
+        out = torch.empty_like(tokens)
+    ext.fullscan_forward_cl(gates, tokens, out, reverse)
+    return out
+
+
+def scan_backward_channel_last(
+    gates: torch.Tensor,
+    out: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_gates: Optional[torch.Tensor] = None,
+    grad_tokens: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gradients of ``scan_forward_channel_last`` given its output: grad_tokens[:, t] =
+    grad_out[:, t] + gates[:, t+1]*grad_tokens[:, t+1] and grad_gates[:, t] =
+    grad_tokens[:, t]*out[:, t-1]. Returns (grad_gates, grad_tokens)."""
+    ext = _load_extension()
+    if grad_gates is None:
+        grad_gates = torch.empty_like(gates)
+    if grad_tokens is None:
+        grad_tokens = torch.empty_like(gates)
+    ext.fullscan_backward_cl(gates, out, grad_out, grad_gates, grad_tokens)
+    return grad_gates, grad_tokens
+
+
+class PScanChannelLast(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+        out = scan_forward_channel_last(gates, tokens)
+        ctx.save_for_backward(gates, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        gates, out = ctx.saved_tensors
+        grad_output = grad_output.contiguous()
+        grad_gates, grad_tokens = scan_backward_channel_last(gates, out, grad_output)
+        return grad_gates, grad_tokens
+
+
+def pscan_channel_last(gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """Differentiable scan of (batch, seqlen, dim) tensors along seqlen."""
+    return PScanChannelLast.apply(gates, tokens)
 
 
 def set_launch_override(waves_per_row: int = 0, ring_depth: int = 0) -> None:

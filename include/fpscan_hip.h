@@ -18,10 +18,10 @@
  *
  * Workspace: large problems run fastest on the tiled path, which needs
  * fpscan_workspace_bytes() bytes of device memory (one 8-byte word per tile plus 1152 bytes
- * of counters, about 0.05 % of one tensor). Pass a buffer of at least that size, 8-byte aligned, owned by the
- * caller and not used by any other call in flight. Its contents are overwritten. With no
- * workspace (or a smaller one) the call takes the row-streaming path instead: same results up
- * to fp32 rounding order, somewhat lower bandwidth. The tiled path is an ordinary launch that
+ * of counters, about 0.05 % of one tensor). Pass a buffer of at least that size, 8-byte
+ * aligned, owned by the caller and not used by any other call in flight. Its contents are
+ * overwritten. With no workspace (or a smaller one) the call takes the row-streaming path
+ * instead: same results up to fp32 rounding order, somewhat lower bandwidth. The tiled path is an ordinary launch that
  * needs no co-residency (workgroups claim tiles in order); if the occupancy query fails, the
  * call streams rows.
  *
@@ -94,6 +94,41 @@ int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out,
  * No reference counterpart: the reference kernel keeps its carries in shared memory
  * (full_scan.cu:55-57). */
 size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype, int op);
+
+/* Channel-last scan: tensors (batch, seqlen, dim) with the dim axis contiguous, element
+ * (b, t, d) at b*stride_b + t*stride_t + d, the recurrence running along seqlen:
+ *   y[b,t,d] = gates[b,t,d] * y[b,t-1,d] + tokens[b,t,d]   (reverse: y[b,t+1,d]).
+ * Same semantics as fpscan_scan_fwd on the transposed data (first gate ignored, zero initial
+ * state, fp32 arithmetic), without the transposes. Any seqlen >= 1; dim, stride_t and
+ * stride_b multiples of 16/itemsize elements; pointers 16-byte aligned; `out` may alias
+ * `tokens` or `gates` exactly. With fewer than 512 strips of 64 16-byte vectors
+ * (batch * dim / (64 * 16/itemsize)) the time axis is cut into segments, which needs
+ * fpscan_workspace_bytes_cl() bytes of workspace; without it the call runs one pass per strip
+ * (correct, slower), except that a batch slab of more than about 2 GiB needs the workspace
+ * (FPSCAN_ERR_WORKSPACE otherwise).
+ * No reference counterpart: the reference supports (batch, dim, seqlen) only and tells callers
+ * of this layout to transpose in and out (README.md:94-99). */
+int fpscan_scan_fwd_cl(const void* gates, const void* tokens, void* out,
+                       int64_t batch, int64_t seqlen, int64_t dim,
+                       int64_t stride_b, int64_t stride_t,
+                       int dtype, int reverse,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused backward of fpscan_scan_fwd_cl (forward direction), given its output `out`:
+ *   grad_tokens[b,t,d] = grad_out[b,t,d] + gates[b,t+1,d] * grad_tokens[b,t+1,d]  (gates[b,L,d] = 1)
+ *   grad_gates[b,t,d]  = grad_tokens[b,t,d] * out[b,t-1,d]                      (out[b,-1,d] = 0)
+ * Same layout rules as fpscan_scan_fwd_cl; outputs must not alias inputs. No reference
+ * counterpart (the reference composes its backward from ATen ops, fpscan/ops.py:69-83). */
+int fpscan_scan_bwd_cl(const void* gates, const void* out, const void* grad_out,
+                       void* grad_gates, void* grad_tokens,
+                       int64_t batch, int64_t seqlen, int64_t dim,
+                       int64_t stride_b, int64_t stride_t,
+                       int dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace, in bytes, for the segmented channel-last path of this problem (0: one pass). */
+size_t fpscan_workspace_bytes_cl(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_t,
+                                 int dtype, int op);
 
 /* Static description of a status code (never NULL). The reference's equivalent is the
  * TORCH_CHECK message text (full_scan.h:7-9). */

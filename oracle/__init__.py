@@ -19,6 +19,10 @@ What each function restates (saeeddhqan/fpscan, paths relative to the reference 
                         op sequence); the CPU baseline bench.py times
   pscan_backward_composed  fpscan/ops.py:69-83: the backward composed from a scan function
                         (shifted gates, reverse scan, shifted output, product)
+  scan_f64_channel_last, scan_bwd_f64_channel_last
+                        the two float64 functions above for (batch, seqlen, dim) tensors
+                        scanned along seqlen (README.md:94-99's transpose-in/transpose-out
+                        recipe, done on the CPU)
 
 How each is pinned (tests/test_oracle.py): closed forms (g = 1 -> cumsum, g = 0 -> x,
 constant g -> geometric series, impulse -> powers of g), brute force from the explicit sum
@@ -26,7 +30,9 @@ y[t] = sum_s (prod_{k=s+1..t} g[k]) x[s], exact rational arithmetic (tests/golde
 float64 autograd through a serial loop and finite differences (gradcheck) for the backward,
 the adjoint identity <go, J v> = <J^T go, v>, and agreement between the two forward
 implementations. ``refkernel_f32`` is pinned against exact results on inputs whose every
-partial result is exactly representable in fp32.
+partial result is exactly representable in fp32. The channel-last pair is pinned against a
+direct loop along axis 1, cumsum along axis 1 for g = 1, and float64 autograd through that
+loop.
 """
 from __future__ import annotations
 
@@ -130,6 +136,23 @@ def scan_bwd_f64(gates, out, grad_out) -> Tuple[np.ndarray, np.ndarray]:
                                     _ptr(go, ctypes.c_double), _ptr(gg, ctypes.c_double),
                                     _ptr(gx, ctypes.c_double), rows, L)
     return gg, gx
+
+
+def scan_f64_channel_last(gates, tokens, reverse: bool = False) -> np.ndarray:
+    """``scan_f64`` for (batch, seqlen, dim) tensors scanned along seqlen: the same
+    recurrences as the (batch, dim, seqlen) transpose, so it transposes, scans and transposes
+    back."""
+    g = np.swapaxes(to_f64(gates), -1, -2)
+    x = np.swapaxes(to_f64(tokens), -1, -2)
+    return np.ascontiguousarray(np.swapaxes(scan_f64(g, x, reverse), -1, -2))
+
+
+def scan_bwd_f64_channel_last(gates, out, grad_out) -> Tuple[np.ndarray, np.ndarray]:
+    """``scan_bwd_f64`` for (batch, seqlen, dim) tensors (see ``scan_f64_channel_last``)."""
+    sw = lambda a: np.swapaxes(to_f64(a), -1, -2)  # noqa: E731
+    gg, gx = scan_bwd_f64(sw(gates), sw(out), sw(grad_out))
+    return (np.ascontiguousarray(np.swapaxes(gg, -1, -2)),
+            np.ascontiguousarray(np.swapaxes(gx, -1, -2)))
 
 
 def refkernel_f32(gates, tokens, reverse: bool = False) -> np.ndarray:

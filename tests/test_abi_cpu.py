@@ -195,3 +195,57 @@ def test_missing_extension_raises_import_error(monkeypatch):
     monkeypatch.setattr(ops, "_EXT_CANDIDATES", ("fpscan_amd._no_such_module",))
     with pytest.raises(ImportError, match="_no_such_module"):
         ops.scan_forward(torch.rand(1, 1, 32), torch.rand(1, 1, 32))
+
+
+# ---------------------------------------------------------------- channel-last C ABI
+@pytest.fixture(scope="module")
+def cl_lib(lib):
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_scan_fwd_cl.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                       ctypes.c_int, vp, ctypes.c_size_t, vp]
+    lib.fpscan_scan_bwd_cl.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                       vp, ctypes.c_size_t, vp]
+    lib.fpscan_workspace_bytes_cl.argtypes = [i64, i64, i64, i64, ctypes.c_int, ctypes.c_int]
+    lib.fpscan_workspace_bytes_cl.restype = ctypes.c_size_t
+    return lib
+
+
+def test_channel_last_validation(cl_lib):
+    d = header_defines()
+    f = cl_lib.fpscan_scan_fwd_cl
+    # (batch, seqlen, dim) = (2, 100, 64), packed strides (stride_b = 6400, stride_t = 64)
+    assert f(FAKE, FAKE, FAKE, 2, 100, 64, 6400, 64, 3, 0, None, 0, None) == d["FPSCAN_ERR_DTYPE"]
+    assert f(FAKE, FAKE, FAKE, -1, 100, 64, 6400, 64, 0, 0, None, 0, None) == d["FPSCAN_ERR_SHAPE"]
+    assert f(FAKE, FAKE, FAKE, 2, 100, 64, 6400, 32, 0, 0, None, 0, None) == d["FPSCAN_ERR_SHAPE"]
+    assert f(FAKE, FAKE, FAKE, 2, 100, 64, 100, 64, 0, 0, None, 0, None) == d["FPSCAN_ERR_SHAPE"]
+    assert f(FAKE, FAKE, FAKE, 2, 100, 62, 6200, 62, 0, 0, None, 0, None) == d["FPSCAN_ERR_ALIGN"]
+    assert f(FAKE, FAKE, FAKE, 2, 100, 60, 6000, 60, 1, 0, None, 0, None) == d["FPSCAN_ERR_ALIGN"]
+    assert f(FAKE + 8, FAKE, FAKE, 2, 100, 64, 6400, 64, 0, 0, None, 0, None) == \
+        d["FPSCAN_ERR_ALIGN"]
+    assert f(None, FAKE, FAKE, 2, 100, 64, 6400, 64, 0, 0, None, 0, None) == d["FPSCAN_ERR_NULL"]
+    assert f(None, None, None, 0, 100, 64, 6400, 64, 0, 0, None, 0, None) == 0  # empty
+    assert f(None, None, None, 2, 0, 64, 0, 64, 0, 0, None, 0, None) == 0
+    b = cl_lib.fpscan_scan_bwd_cl
+    assert b(FAKE, FAKE, FAKE, FAKE, None, 2, 100, 64, 6400, 64, 0, None, 0, None) == \
+        d["FPSCAN_ERR_NULL"]
+
+
+def test_channel_last_workspace_plan(cl_lib):
+    """One pass when batch x strips (64 16-byte vectors each) reaches 512; otherwise segments
+    of >= 64 steps aiming at 8192 wave tasks, one (A, B) pair of 8 bytes per segment per
+    column."""
+    w = cl_lib.fpscan_workspace_bytes_cl
+    assert w(64, 1024, 8192, 8192, 0, 0) == 0  # 64 x 32 strips: one pass
+    assert w(64, 256, 4096, 4096, 0, 0) == 0  # config 5 in channel-last form: 1024 strips
+    assert w(16, 4096, 8192, 8192, 0, 0) == 0  # 512 strips
+    assert w(1, 100, 64, 64, 0, 0) == 0  # too short to cut (< 2 segments of 64)
+    # bf16 (8, 65536, 1024): 8 x 2 strips -> 512 segments of 128 steps
+    assert w(8, 65536, 1024, 1024, 2, 0) == 512 * 8 * 1024 * 8
+    assert w(8, 65536, 1024, 1024, 2, 1) == 512 * 8 * 1024 * 8
+    # fp32 (4, 4096, 8192): 4 x 32 strips -> 64 segments of 64 steps
+    assert w(4, 4096, 8192, 8192, 0, 0) == 64 * 4 * 8192 * 8
+    # capped by seqlen / 64 segments: fp32 (1, 1000, 64) -> 15 segments of 67 steps
+    assert w(1, 1000, 64, 64, 0, 0) == 15 * 1 * 64 * 8
+    assert w(1, 100, 64, 64, 0, 7) == 0  # unknown op
+    assert w(1, 100, 64, 64, 5, 0) == 0  # unknown dtype
+    assert w(1, 100, 64, 32, 0, 0) == 0  # stride_t < dim

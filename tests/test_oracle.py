@@ -270,3 +270,57 @@ def test_normwise_error_definition():
     ref = np.array([[1.0, -4.0, 2.0]])
     assert oracle.normwise_error(ref + np.array([[0.0, 0.4, 0.0]]), ref) == pytest.approx(0.1)
     assert oracle.normwise_error(np.zeros((1, 3)), np.zeros((1, 3))) == 0.0
+
+
+# ---------------------------------------------------------------- channel-last helpers
+def _loop_axis1(g, x, reverse=False):
+    """The channel-last definition written out: state per (batch, column), stepped along
+    axis 1 (seqlen) in processing order."""
+    B, L, D = x.shape
+    y = np.empty_like(x)
+    state = np.zeros((B, D))
+    ts = range(L - 1, -1, -1) if reverse else range(L)
+    for t in ts:
+        state = g[:, t, :] * state + x[:, t, :]
+        y[:, t, :] = state
+    return y
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("shape", [(1, 1, 1), (2, 5, 3), (3, 33, 8), (1, 100, 17)])
+def test_channel_last_matches_direct_loop_along_seqlen(shape, reverse):
+    rng = np.random.default_rng(sum(shape))
+    g = rng.uniform(-1.2, 1.2, size=shape)
+    x = rng.standard_normal(size=shape)
+    y = oracle.scan_f64_channel_last(g, x, reverse)
+    np.testing.assert_allclose(y, _loop_axis1(g, x, reverse), rtol=1e-13, atol=1e-13)
+
+
+def test_channel_last_closed_forms():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 40, 6))
+    ones = np.ones_like(x)
+    np.testing.assert_allclose(oracle.scan_f64_channel_last(ones, x), np.cumsum(x, axis=1),
+                               rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oracle.scan_f64_channel_last(ones, x, reverse=True),
+                               np.cumsum(x[:, ::-1], axis=1)[:, ::-1], rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(oracle.scan_f64_channel_last(np.zeros_like(x), x), x)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 2), (2, 7, 3), (1, 32, 5)])
+def test_channel_last_backward_matches_torch_autograd(shape):
+    rng = np.random.default_rng(7 + sum(shape))
+    g = rng.uniform(-1.2, 1.2, size=shape)
+    x = rng.standard_normal(size=shape)
+    go = rng.standard_normal(size=shape)
+    gt = torch.tensor(g, requires_grad=True)
+    xt = torch.tensor(x, requires_grad=True)
+    state = torch.zeros(shape[0], shape[2], dtype=torch.float64)
+    outs = []
+    for t in range(shape[1]):
+        state = gt[:, t, :] * state + xt[:, t, :]
+        outs.append(state)
+    (torch.stack(outs, dim=1) * torch.tensor(go)).sum().backward()
+    gg, gx = oracle.scan_bwd_f64_channel_last(g, oracle.scan_f64_channel_last(g, x), go)
+    np.testing.assert_allclose(gx, xt.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(gg, gt.grad.numpy(), rtol=1e-12, atol=1e-12)
