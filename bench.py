@@ -365,12 +365,40 @@ def bench_channel_last(args):
     return entry
 
 
+def bench_dimwise(args):
+    """dw: dimwise_forward (the reference module's contraction scan) at the headline shape,
+    B8 D1024 L65536; 3 N s bytes per call (read Ax and Bx, write Bx; Bh, Wq, Wk are
+    negligible). The reference's inputs (scans/contraction_scan.py:154-159)."""
+    import fpscan_amd
+
+    B, D, L = 8, 1024, 65536
+    dtype = DTYPES[args.dtype or "bfloat16"]
+    s = torch.empty((), dtype=dtype).element_size()
+    N = B * D * L
+    G = fpscan_amd.dimwise_groups(L)
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    ax = (0.99 + 0.01 * torch.rand(B, D, L, generator=gen, device="cuda")).to(dtype)
+    bx0 = (torch.randn(B, D, L, generator=gen, device="cuda") / G).to(dtype)
+    bh = (torch.randn(B, D, G, generator=gen, device="cuda") / G).to(dtype)
+    wq = (0.01 * torch.rand(D, generator=gen, device="cuda")).to(dtype)
+    wk = (0.01 * torch.rand(D, generator=gen, device="cuda")).to(dtype)
+    bx = bx0.clone()
+    # in place: each call scans the previous call's output, which is the same work
+    t = time_each(lambda: fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk), 5, args.iters)
+    p50 = percentile(t, 0.5)
+    entry = {"workload": "dw: dimwise_forward B8 D1024 L65536", "dtype": SHORT[dtype],
+             "p50_ms": round(p50, 5), "gbps": round(3 * N * s / (p50 / 1e3) / 1e9, 1),
+             "hbm_frac": round(3 * N * s / (p50 / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    print(json.dumps(entry), flush=True)
+    return entry
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl"])
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw"])
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -409,6 +437,8 @@ def main():
         res = bench_sweep(args)
     elif args.workload.endswith("cl"):
         res = bench_channel_last(args)
+    elif args.workload == "dw":
+        res = bench_dimwise(args)
     else:
         res = bench_shape(args)
     print(json.dumps(res), flush=True)

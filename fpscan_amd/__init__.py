@@ -3,11 +3,14 @@
 Same public names as fpscan/__init__.py:1-3 (``pscan``, ``scan_forward``, ``PScan``), plus
 ``scan_backward`` (the fused backward, exposed directly) and the channel-last variants for
 (batch, seqlen, dim) tensors (``pscan_channel_last``, ``scan_forward_channel_last``,
-``scan_backward_channel_last``, ``PScanChannelLast``).
+``scan_backward_channel_last``, ``PScanChannelLast``), and ``dimwise_forward`` (the
+reference module's contraction scan, csrc/main.cpp:10) with ``dimwise_groups``.
 """
-from .ops import (PScan, PScanChannelLast, pscan, pscan_channel_last, scan_backward,
-                  scan_backward_channel_last, scan_forward, scan_forward_channel_last)
+from .ops import (PScan, PScanChannelLast, dimwise_forward, dimwise_groups, pscan,
+                  pscan_channel_last, scan_backward, scan_backward_channel_last, scan_forward,
+                  scan_forward_channel_last)
 
 __all__ = ["pscan", "scan_forward", "scan_backward", "PScan", "pscan_channel_last",
-           "scan_forward_channel_last", "scan_backward_channel_last", "PScanChannelLast"]
+           "scan_forward_channel_last", "scan_backward_channel_last", "PScanChannelLast",
+           "dimwise_forward", "dimwise_groups"]
 __version__ = "0.2.0"

@@ -8,7 +8,8 @@
 //                                current stream
 // Added: `fullscan_backward`, the fused backward that replaces the composition in
 // fpscan/ops.py:69-83, plus the checks the reference leaves out (shapes, `out`, device);
-// `fullscan_forward_cl` / `fullscan_backward_cl` for (batch, seqlen, dim) tensors.
+// `fullscan_forward_cl` / `fullscan_backward_cl` for (batch, seqlen, dim) tensors;
+// `dimwise_forward` (csrc/main.cpp:10), the contraction scan.
 // Every check runs before any HIP call, so a bad call raises RuntimeError on any machine.
 #include <torch/extension.h>
 
@@ -18,6 +19,7 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <string>
+#include <utility>
 
 #include "fpscan_hip.h"
 
@@ -213,6 +215,45 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward_cl(const at::Tensor& gates,
   return {grad_gates, grad_tokens};
 }
 
+// ---- dimwise_forward: csrc/main.cpp:10, csrc/dimwise/dimwise.h:27-42 (CHECK_INPUT on all
+// five tensors, same messages), in place into Bx, returns nothing. Added checks: one dtype
+// for all five (the reference reinterprets Bh/Wq/Wk as Ax's type), the shapes of Ax, Bh,
+// Wq and Wk (the reference reads out of bounds when they are short).
+void dimwise_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tensor& Bh,
+                     const at::Tensor& Wq, const at::Tensor& Wk) {
+  for (const auto& [t, name] : {std::pair<const at::Tensor*, const char*>{&Ax, "Ax"},
+                                {&Bx, "Bx"}, {&Bh, "Bh"}, {&Wq, "Wq"}, {&Wk, "Wk"}}) {
+    TORCH_CHECK(t->device().is_cuda(), name, " must be a CUDA tensor");
+    TORCH_CHECK(t->is_contiguous(), name, " must be contiguous");
+    const auto st = t->scalar_type();
+    TORCH_CHECK(st == at::kHalf || st == at::kBFloat16 || st == at::kFloat, name,
+                " must be float16 or bfloat16 or float32");
+    TORCH_CHECK(st == Bx.scalar_type(), name, " must have the dtype of Bx (", Bx.scalar_type(),
+                "), got ", st);
+    TORCH_CHECK(t->device() == Bx.device(), name, " must be on ", Bx.device());
+  }
+  TORCH_CHECK(Bx.dim() == 3, "Bx must be a 3-d (batch, dim, seqlen) tensor, got ", Bx.dim(),
+              " dims");
+  TORCH_CHECK(Ax.sizes() == Bx.sizes(), "Ax must have the shape of Bx ", Bx.sizes(), ", got ",
+              Ax.sizes());
+  const int64_t B = Bx.size(0), D = Bx.size(1), L = Bx.size(2);
+  const int G = fpscan_dimwise_groups(L);
+  TORCH_CHECK(G > 0, "seqlen must be a power of 2, >= 64, <= 65536, got ", L);
+  TORCH_CHECK(Bh.dim() == 3 && Bh.size(0) == B && Bh.size(1) == D && Bh.size(2) == G,
+              "Bh must have shape (", B, ", ", D, ", ", G, ") for seqlen ", L, ", got ",
+              Bh.sizes());
+  TORCH_CHECK(Wq.numel() == D && Wk.numel() == D, "Wq and Wk must have ", D,
+              " elements (one per dim), got ", Wq.numel(), " and ", Wk.numel());
+  if (Bx.numel() == 0) return;
+
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
+  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(Bx.device().index()).stream();
+  const int status = fpscan_dimwise_fwd(Ax.data_ptr(), Bx.data_ptr(), Bh.data_ptr(),
+                                        Wq.data_ptr(), Wk.data_ptr(), B, D, L,
+                                        dtype_code(Bx.scalar_type()), stream);
+  check_status(status);
+}
+
 int set_launch_override(int waves_per_row, int ring_depth) {
   const int status = fpscan_set_launch_override(waves_per_row, ring_depth);
   TORCH_CHECK(status == FPSCAN_OK, "waves_per_row must be one of 0,1,2,4,8,16 and ring_depth "
@@ -237,6 +278,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "fused backward of the channel-last forward scan: (grad_gates, grad_tokens)",
         pybind11::arg("gates"), pybind11::arg("out"), pybind11::arg("grad_out"),
         pybind11::arg("grad_gates"), pybind11::arg("grad_tokens"));
+  m.def("dimwise_forward", &dimwise_forward,
+        "contraction scan, in place into Bx (HIP, gfx950)", pybind11::arg("Ax"),
+        pybind11::arg("Bx"), pybind11::arg("Bh"), pybind11::arg("Wq"), pybind11::arg("Wk"));
+  m.def("dimwise_groups", &fpscan_dimwise_groups,
+        "Bh entries per row expected by dimwise_forward for this seqlen (0: unsupported)",
+        pybind11::arg("seqlen"));
   m.def("set_launch_override", &set_launch_override,
         "tuning hook: force waves per row / ring depth (0 = built-in choice)",
         pybind11::arg("waves_per_row"), pybind11::arg("ring_depth"));

@@ -124,6 +124,86 @@ __device__ __forceinline__ void bst16(Rsrc r, uint32_t off, u32x4 v) {
 // Byte offset that no row range contains: loads from it return 0 without touching memory.
 constexpr uint32_t kNoOffset = 0x80000000u;
 
+// ---------------------------------------------------------------------------------------
+// Wave64 lane movement (DPP). Lanes whose source is outside the row / wave, or whose row is
+// masked off, keep `old`.
+// ---------------------------------------------------------------------------------------
+constexpr int kRowShr1 = 0x111;
+constexpr int kRowShr2 = 0x112;
+constexpr int kRowShr4 = 0x114;
+constexpr int kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142;
+constexpr int kRowBcast31 = 0x143;
+constexpr int kWaveShl1 = 0x130;
+constexpr int kWaveShr1 = 0x138;
+
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float dpp(float old, float src) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
+                                         kCtrl, kRowMask, 0xf, false));
+}
+
+// Workgroup barrier that orders LDS only. __syncthreads() is a workgroup-scope fence on all
+// memory, which on gfx9 waits for every outstanding global load -- it would drain the operand
+// ring at each barrier. The barriers here guard LDS exchanges only: operands are read-only
+// and every output element is written by the lane that read its inputs.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// (A, B) := (earlier) o (A, B): the earlier lane's map is applied first.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ void combine_from(float& A, float& B) {
+  const float pA = dpp<kCtrl, kRowMask>(1.0f, A);
+  const float pB = dpp<kCtrl, kRowMask>(0.0f, B);
+  B = fmaf(pB, A, B);
+  A = pA * A;
+}
+
+// Same, but lanes with !ok combine with the identity (segments narrower than a DPP row).
+template <int kCtrl>
+__device__ __forceinline__ void combine_from_masked(float& A, float& B, bool ok) {
+  float pA = dpp<kCtrl>(1.0f, A);
+  float pB = dpp<kCtrl>(0.0f, B);
+  pA = ok ? pA : 1.0f;
+  pB = ok ? pB : 0.0f;
+  B = fmaf(pB, A, B);
+  A = pA * A;
+}
+
+// Inclusive scan over all 64 lanes.
+__device__ __forceinline__ void wave_scan(float& A, float& B) {
+  combine_from<kRowShr1>(A, B);
+  combine_from<kRowShr2>(A, B);
+  combine_from<kRowShr4>(A, B);
+  combine_from<kRowShr8>(A, B);
+  combine_from<kRowBcast15, 0xa>(A, B);  // lane 15 -> row 1, lane 47 -> row 3
+  combine_from<kRowBcast31, 0xc>(A, B);  // lane 31 -> rows 2 and 3
+}
+
+// Inclusive scan inside aligned segments of G lanes (G in {4, 8, 16, 32}); sl = lane % G.
+template <int G>
+__device__ __forceinline__ void segment_scan(float& A, float& B, int sl) {
+  if constexpr (G >= 16) {
+    combine_from<kRowShr1>(A, B);
+    combine_from<kRowShr2>(A, B);
+    combine_from<kRowShr4>(A, B);
+    combine_from<kRowShr8>(A, B);
+    if constexpr (G == 32) combine_from<kRowBcast15, 0xa>(A, B);
+  } else {
+    combine_from_masked<kRowShr1>(A, B, sl >= 1);
+    combine_from_masked<kRowShr2>(A, B, sl >= 2);
+    if constexpr (G == 8) combine_from_masked<kRowShr4>(A, B, sl >= 4);
+  }
+}
+
 }  // namespace
 
 #endif  // FPSCAN_SCAN_COMMON_H

@@ -169,6 +169,23 @@ def pscan_channel_last(gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tenso
     return PScanChannelLast.apply(gates, tokens)
 
 
+# ---------------------------------------------------------------------------------------
+# Contraction scan: the reference module's dimwise_forward (csrc/main.cpp:10), used by its
+# scans/contraction_scan.py. In place into Bx, returns None, no backward (as the reference).
+# ---------------------------------------------------------------------------------------
+def dimwise_forward(Ax: torch.Tensor, Bx: torch.Tensor, Bh: torch.Tensor, Wq: torch.Tensor,
+                    Wk: torch.Tensor) -> None:
+    """Group scans of (batch, dim, seqlen) rows mixed across groups by a first-maximum
+    selection over (1+Wk)*Bh and (1+Wq)*v, written into Bx. Bh is (batch, dim,
+    dimwise_groups(seqlen)); Wq and Wk have one entry per dim."""
+    _load_extension().dimwise_forward(Ax, Bx, Bh, Wq, Wk)
+
+
+def dimwise_groups(seqlen: int) -> int:
+    """Bh entries per row that dimwise_forward expects for ``seqlen`` (0: unsupported)."""
+    return int(_load_extension().dimwise_groups(int(seqlen)))
+
+
 def set_launch_override(waves_per_row: int = 0, ring_depth: int = 0) -> None:
     """Tuning hook: force the number of waves per row and the per-wave ring depth of the
     long-row kernels (0 restores the built-in choice). Process-wide."""

@@ -130,6 +130,27 @@ int fpscan_scan_bwd_cl(const void* gates, const void* out, const void* grad_out,
 size_t fpscan_workspace_bytes_cl(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_t,
                                  int dtype, int op);
 
+/* Contraction scan, in place into `tokens` (the reference's Bx):
+ * replaces dimwise_forward / dimwise_fwd / dimwise_pscan (csrc/main.cpp:10,
+ * csrc/dimwise/dimwise.h:27-42, csrc/dimwise/dimwise_scan_final.cu:387-576).
+ * gates/tokens: (batch, dim, seqlen) contiguous; bh: (batch, dim, G) contiguous with
+ * G = fpscan_dimwise_groups(seqlen); wq, wk: dim elements. All five share `dtype`.
+ * seqlen a power of two in [64, 65536] (the reference rejects 32 and everything else too).
+ * Per row, in chunks of W groups: zero-initial-state group scans (group 0 continues from the
+ * previous chunk), then each group g >= 1 adds r[g-1], where r mixes the group ends v through
+ * a first-maximum selection of (1+Wk)*Bh[h] * (1+Wq)*v[g] over earlier groups h. fp32
+ * arithmetic with one rounding, except the selection's k, q and scores, which are rounded as
+ * the reference rounds them in the tensors' type. Runs on `stream` (the reference uses the
+ * legacy default stream). No workspace, no backward (the reference has none). */
+int fpscan_dimwise_fwd(const void* gates, void* tokens, const void* bh, const void* wq,
+                       const void* wk, int64_t batch, int64_t dim, int64_t seqlen, int dtype,
+                       void* stream);
+
+/* Number of Bh entries per row (G = W * C) that fpscan_dimwise_fwd expects for this seqlen,
+ * 0 if seqlen is not supported. Only the first W (<= 32) are read: the reference indexes Bh
+ * without the chunk (dimwise_scan_final.cu:133, :189). */
+int fpscan_dimwise_groups(int64_t seqlen);
+
 /* Static description of a status code (never NULL). The reference's equivalent is the
  * TORCH_CHECK message text (full_scan.h:7-9). */
 const char* fpscan_strerror(int status);

@@ -19,6 +19,8 @@ What each function restates (saeeddhqan/fpscan, paths relative to the reference 
                         op sequence); the CPU baseline bench.py times
   pscan_backward_composed  fpscan/ops.py:69-83: the backward composed from a scan function
                         (shifted gates, reverse scan, shifted output, product)
+  dimwise_f64           csrc/dimwise/dimwise_scan_final.cu:12-576 -- the contraction scan
+                        behind dimwise_forward, in float64 (numpy)
   scan_f64_channel_last, scan_bwd_f64_channel_last
                         the two float64 functions above for (batch, seqlen, dim) tensors
                         scanned along seqlen (README.md:94-99's transpose-in/transpose-out
@@ -32,7 +34,9 @@ the adjoint identity <go, J v> = <J^T go, v>, and agreement between the two forw
 implementations. ``refkernel_f32`` is pinned against exact results on inputs whose every
 partial result is exactly representable in fp32. The channel-last pair is pinned against a
 direct loop along axis 1, cumsum along axis 1 for g = 1, and float64 autograd through that
-loop.
+loop. ``dimwise_f64`` is pinned against a restatement of the reference's own Python model of
+the same computation (scans/contraction_scan.py:98-142, a per-token loop with torch.max for
+the selection), against group-sum closed forms, and on ties.
 """
 from __future__ import annotations
 
@@ -153,6 +157,65 @@ def scan_bwd_f64_channel_last(gates, out, grad_out) -> Tuple[np.ndarray, np.ndar
     gg, gx = scan_bwd_f64(sw(gates), sw(out), sw(grad_out))
     return (np.ascontiguousarray(np.swapaxes(gg, -1, -2)),
             np.ascontiguousarray(np.swapaxes(gx, -1, -2)))
+
+
+# (W groups per chunk, P elements per group, C chunks) by seqlen: the reference launcher's
+# kernel table, csrc/dimwise/dimwise_scan_final.cu:408-572 (seqlen 32 and others rejected).
+DIMWISE_GEOMETRY = {64: (2, 32, 1), 128: (4, 32, 1), 256: (8, 32, 1), 512: (16, 32, 1),
+                    1024: (16, 64, 1), 2048: (32, 64, 1), 4096: (32, 128, 1),
+                    8192: (32, 128, 2), 16384: (32, 128, 4), 32768: (32, 128, 8),
+                    65536: (32, 128, 16)}
+
+
+def dimwise_f64(Ax, Bx, Bh, Wq, Wk) -> np.ndarray:
+    """float64 result of the reference's dimwise_forward (the value it writes into Bx).
+
+    Restates csrc/dimwise/dimwise_scan_final.cu:108-225 (the other kernels are its one-chunk
+    cases), per row (b, d): chunks of W groups of P elements; zero-initial-state scans inside
+    each group, group 0 starting from the previous chunk's last output (:153-159); v = group
+    ends; k = (1+Wk)*Bh[..., :W] (chunk index unused, :133, :189); q = (1+Wq)*v; r[0] = v[0],
+    r[g] = s*v[m] + v[g] for 1 <= g <= W-2 with s = k[m]*q[g] the first strict maximum over
+    h < g above -1e10 (:195-210; m = 0 where the reference leaves it undefined); outputs
+    local + r[g-1] for g >= 1 (:213-219). Ax, Bx: (batch, dim, seqlen); Bh: (batch, dim, W*C);
+    Wq, Wk: dim values.
+    """
+    a, x = to_f64(Ax), to_f64(Bx)
+    B, D, L = x.shape
+    W, P, C = DIMWISE_GEOMETRY[L]
+    k = (1.0 + to_f64(Wk).reshape(1, D, 1)) * to_f64(Bh).reshape(B, D, W * C)[:, :, :W]
+    wq1 = 1.0 + to_f64(Wq).reshape(1, D)
+    out = np.empty_like(x)
+    carry = np.zeros((B, D))
+    for c in range(C):
+        span = slice(c * W * P, (c + 1) * W * P)
+        ac = a[:, :, span].reshape(B, D, W, P).copy()
+        xc = x[:, :, span].reshape(B, D, W, P)
+        if c == 0:
+            ac[:, :, 0, 0] = 1.0  # the row's first gate is never used (:151)
+        y = np.zeros((B, D, W))
+        y[:, :, 0] = carry
+        local = np.empty((B, D, W, P))
+        for j in range(P):
+            y = ac[..., j] * y + xc[..., j]
+            local[..., j] = y
+        v = local[..., P - 1]
+        r = v.copy()
+        for g in range(1, W - 1):
+            q = wq1 * v[:, :, g]
+            best = np.full((B, D), -1e10)
+            m = np.zeros((B, D), dtype=np.int64)
+            for h in range(g):
+                s = k[:, :, h] * q
+                better = s > best
+                best = np.where(better, s, best)
+                m = np.where(better, h, m)
+            vm = np.take_along_axis(v, m[..., None], axis=2)[..., 0]
+            r[:, :, g] = best * vm + v[:, :, g]
+        outc = local.copy()
+        outc[:, :, 1:, :] += r[:, :, :-1, None]
+        out[:, :, span] = outc.reshape(B, D, W * P)
+        carry = outc[:, :, W - 1, P - 1]
+    return out
 
 
 def refkernel_f32(gates, tokens, reverse: bool = False) -> np.ndarray:

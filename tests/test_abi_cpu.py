@@ -249,3 +249,22 @@ def test_channel_last_workspace_plan(cl_lib):
     assert w(1, 100, 64, 64, 0, 7) == 0  # unknown op
     assert w(1, 100, 64, 64, 5, 0) == 0  # unknown dtype
     assert w(1, 100, 64, 32, 0, 0) == 0  # stride_t < dim
+
+
+# ---------------------------------------------------------------- dimwise C ABI
+def test_dimwise_groups_and_validation(lib):
+    d = header_defines()
+    lib.fpscan_dimwise_groups.argtypes = [ctypes.c_int64]
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    f = lib.fpscan_dimwise_fwd
+    f.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_int, vp]
+    # G = W * C per seqlen (dimwise_scan_final.cu:408-572); 32 and non-powers rejected
+    want = {64: 2, 128: 4, 256: 8, 512: 16, 1024: 16, 2048: 32, 4096: 32, 8192: 64,
+            16384: 128, 32768: 256, 65536: 512, 32: 0, 96: 0, 131072: 0}
+    assert {L: lib.fpscan_dimwise_groups(L) for L in want} == want
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 32, 0, None) == d["FPSCAN_ERR_SEQLEN"]
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 64, 3, None) == d["FPSCAN_ERR_DTYPE"]
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, -1, 4, 64, 0, None) == d["FPSCAN_ERR_SHAPE"]
+    assert f(FAKE, None, FAKE, FAKE, FAKE, 2, 4, 64, 0, None) == d["FPSCAN_ERR_NULL"]
+    assert f(FAKE + 4, FAKE, FAKE, FAKE, FAKE, 2, 4, 64, 0, None) == d["FPSCAN_ERR_ALIGN"]
+    assert f(None, None, None, None, None, 0, 4, 64, 0, None) == 0  # empty

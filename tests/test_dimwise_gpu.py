@@ -1,0 +1,151 @@
+"""GPU parity tests of dimwise_forward (the reference module's contraction scan,
+csrc/main.cpp:10, csrc/dimwise/) against the float64 oracle (oracle.dimwise_f64, pinned in
+tests/test_oracle.py by a restatement of the reference's own Python model).
+
+The reference's only check of this function is scans/contraction_scan.py:144-185 (fp32,
+atol 1e-3 against its Python model); here every supported seqlen runs in every dtype, with
+the north-star normwise tolerances. The selection (a first maximum) is discontinuous, so the
+half-precision cases draw keys that are well apart and group sums of one sign: the same group
+is then chosen in any precision, as it must be for results to agree at all.
+"""
+import numpy as np
+import pytest
+import torch
+
+import fpscan_amd
+import oracle
+from scan_helpers import DEVICE, DTYPES, check
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a HIP device (MI355X)"),
+]
+
+SEQLENS = sorted(oracle.DIMWISE_GEOMETRY)
+
+
+def driver_inputs(B, D, L, seed=0):
+    """scans/contraction_scan.py:154-159: Ax 0.99 + 0.01 U, Bx N/G, Bh N/G, Wq/Wk 0.01 U."""
+    W, P, C = oracle.DIMWISE_GEOMETRY[L]
+    G = W * C
+    gen = torch.Generator().manual_seed(seed)
+    ax = 0.99 + 0.01 * torch.rand(B, D, L, generator=gen)
+    bx = torch.randn(B, D, L, generator=gen) / G
+    bh = torch.randn(B, D, G, generator=gen) / G
+    wq = 0.01 * torch.rand(D, generator=gen)
+    wk = 0.01 * torch.rand(D, generator=gen)
+    return ax, bx, bh, wq, wk
+
+
+def separated_inputs(B, D, L, sign=1.0, seed=0):
+    """Keys a permutation of evenly spaced values per row (about 6 % apart), tokens of one
+    sign (so every q has that sign): the selection is unambiguous in fp16 and bf16 too."""
+    W, P, C = oracle.DIMWISE_GEOMETRY[L]
+    G = W * C
+    gen = torch.Generator().manual_seed(seed)
+    ax = 0.99 + 0.01 * torch.rand(B, D, L, generator=gen)
+    bx = sign * (0.5 + 0.5 * torch.rand(B, D, L, generator=gen)) / P
+    ranks = torch.rand(B, D, W, generator=gen).argsort(dim=-1).argsort(dim=-1).double()
+    bh = torch.randn(B, D, G, generator=gen) / G
+    bh[:, :, :W] = (-1.0 + 2.0 * ranks / max(W - 1, 1)) / 4
+    wq = 0.01 * torch.rand(D, generator=gen)
+    wk = 0.01 * torch.rand(D, generator=gen)
+    return ax, bx, bh.float(), wq, wk
+
+
+def run(ax, bx, bh, wq, wk, dtype):
+    t = [v.to(dtype).contiguous() for v in (ax, bx, bh, wq, wk)]
+    want = oracle.dimwise_f64(*t)
+    dev = [v.to(DEVICE) for v in t]
+    assert fpscan_amd.dimwise_forward(*dev) is None  # in place, returns nothing
+    return dev[1], want
+
+
+@pytest.mark.parametrize("L", SEQLENS)
+def test_fp32_driver_distribution_matches_oracle(L):
+    got, want = run(*driver_inputs(2, 4, L, seed=L), torch.float32)
+    check(got, want, torch.float32, f"dimwise fp32 L{L}")
+    # the reference's own bar (scans/contraction_scan.py:184)
+    assert np.abs(got.double().cpu().numpy() - want).max() < 1e-3
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("L", SEQLENS)
+@pytest.mark.parametrize("sign", [1.0, -1.0], ids=["q>0", "q<0"])
+def test_separated_keys_match_oracle(L, dtype, sign):
+    got, want = run(*separated_inputs(2, 3, L, sign=sign, seed=L + 7), dtype)
+    check(got, want, dtype, f"dimwise {dtype} L{L} sign {sign}")
+
+
+@pytest.mark.parametrize("L", [64, 4096, 16384])
+def test_unit_gates_zero_keys_exact(L):
+    """Gates 1, k = 0, integer tokens: every partial result is an exact integer, so the
+    output must equal the oracle bit for bit (group cumsums plus the previous group's total,
+    group 0 continuing from the chunk carry)."""
+    W, P, C = oracle.DIMWISE_GEOMETRY[L]
+    gen = torch.Generator().manual_seed(L)
+    x = torch.randint(-4, 5, (2, 3, L), generator=gen).float()
+    ones = torch.ones_like(x)
+    got, want = run(ones, x, torch.zeros(2, 3, W * C), torch.zeros(3), torch.zeros(3),
+                    torch.float32)
+    assert torch.equal(got.cpu().double(), torch.from_numpy(want))
+
+
+def test_first_gate_is_ignored():
+    ax, bx, bh, wq, wk = driver_inputs(1, 2, 4096, seed=3)
+    axn = ax.clone()
+    axn[:, :, 0] = float("nan")
+    got, _ = run(axn, bx, bh, wq, wk, torch.float32)
+    ref, _ = run(ax, bx, bh, wq, wk, torch.float32)
+    assert torch.equal(got, ref)
+
+
+def test_shapes_and_rows():
+    """Ragged row counts and a single row."""
+    for B, D in [(1, 1), (3, 5), (7, 33)]:
+        got, want = run(*driver_inputs(B, D, 8192, seed=B * D), torch.float32)
+        check(got, want, torch.float32, f"dimwise B{B} D{D}")
+
+
+def test_empty_and_validation():
+    x = torch.rand(2, 3, 64, device=DEVICE)
+    bh = torch.rand(2, 3, 2, device=DEVICE)
+    w = torch.rand(3, device=DEVICE)
+    fpscan_amd.dimwise_forward(x[:0], x[:0].clone(), bh[:0], w, w)  # empty: nothing to do
+    for L in (32, 96, 131072):
+        y = torch.rand(1, 1, L, device=DEVICE)
+        with pytest.raises(RuntimeError, match="seqlen"):
+            fpscan_amd.dimwise_forward(y, y.clone(), torch.rand(1, 1, 2, device=DEVICE),
+                                       w[:1], w[:1])
+    with pytest.raises(RuntimeError, match="Bh must have shape"):
+        fpscan_amd.dimwise_forward(x, x.clone(), torch.rand(2, 3, 4, device=DEVICE), w, w)
+    with pytest.raises(RuntimeError, match="Wq and Wk"):
+        fpscan_amd.dimwise_forward(x, x.clone(), bh, w[:2], w)
+    with pytest.raises(RuntimeError, match="dtype"):
+        fpscan_amd.dimwise_forward(x, x.clone(), bh.half(), w, w)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        fpscan_amd.dimwise_forward(x, x.clone().transpose(0, 1), bh, w, w)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        fpscan_amd.dimwise_forward(x.cpu(), x.clone(), bh, w, w)
+    assert fpscan_amd.dimwise_groups(65536) == 512 and fpscan_amd.dimwise_groups(32) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_headline_shape_b8_d1024_l65536(dtype):
+    """The headline shape: sampled rows against the oracle (all rows run on the GPU)."""
+    gen = torch.Generator(device=DEVICE).manual_seed(11)
+    B, D, L = 8, 1024, 65536
+    ax = (0.99 + 0.01 * torch.rand(B, D, L, generator=gen, device=DEVICE)).to(dtype)
+    bx = ((0.5 + 0.5 * torch.rand(B, D, L, generator=gen, device=DEVICE)) / 128).to(dtype)
+    ranks = torch.rand(B, D, 32, generator=gen, device=DEVICE).argsort(-1).argsort(-1).float()
+    bh = torch.randn(B, D, 512, generator=gen, device=DEVICE) / 512
+    bh[:, :, :32] = (-1.0 + 2.0 * ranks / 31) / 4
+    bh = bh.to(dtype)
+    wq = (0.01 * torch.rand(D, generator=gen, device=DEVICE)).to(dtype)
+    wk = (0.01 * torch.rand(D, generator=gen, device=DEVICE)).to(dtype)
+    rows = [0, 1, 1023, 4096, 8191]
+    sel = lambda t: t.reshape(B * D, -1)[rows].reshape(1, len(rows), -1).cpu()  # noqa: E731
+    want = oracle.dimwise_f64(sel(ax), sel(bx), sel(bh), wq.cpu()[[r % D for r in rows]],
+                              wk.cpu()[[r % D for r in rows]])
+    fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk)
+    check(sel(bx), want, dtype, f"dimwise headline {dtype}")

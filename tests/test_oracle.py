@@ -324,3 +324,100 @@ def test_channel_last_backward_matches_torch_autograd(shape):
     gg, gx = oracle.scan_bwd_f64_channel_last(g, oracle.scan_f64_channel_last(g, x), go)
     np.testing.assert_allclose(gx, xt.grad.numpy(), rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(gg, gt.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- dimwise (contraction scan)
+def _contraction_model(Ax, Bx, kBh, wq1, G, C):
+    """The reference's own Python model of the contraction scan (scans/contraction_scan.py:
+    98-142), restated in float64 torch: (batch, seqlen, dim) layout, a per-token loop inside
+    each group, torch.max over the scores per dim. kBh holds k per (batch, group, dim) and
+    wq1 the factor that makes q from v (the model's arguments kBh and Wq; the kernel's
+    (1+Wk)*Bh and (1+Wq) are passed in, as the model's caller would)."""
+    B, T, Dm = Ax.shape
+    per, wc = T // G, G // C
+    out = torch.empty(B, T, Dm, dtype=torch.float64)
+    carry = None
+    for c in range(C):
+        ends = []
+        for gi in range(wc):
+            first = (c * wc + gi) * per
+            state = torch.zeros(B, Dm, dtype=torch.float64)
+            for t in range(first, first + per):
+                prev = carry if (c > 0 and gi == 0 and t == first) else state
+                state = Ax[:, t] * prev + Bx[:, t]
+                out[:, t] = state
+            ends.append(state)
+        v = torch.stack(ends, dim=1)
+        q = wq1 * v
+        r = v.clone()
+        for gi in range(1, wc - 1):
+            best, idx = torch.max(q[:, gi:gi + 1, :] * kBh[:, :gi, :], dim=1)
+            r[:, gi] = torch.gather(v, 1, idx[:, None, :])[:, 0] * best + v[:, gi]
+        for gi in range(1, wc):
+            s = (c * wc + gi) * per
+            out[:, s:s + per] += r[:, gi - 1][:, None, :]
+        carry = out[:, (c + 1) * wc * per - 1]
+    return out
+
+
+@pytest.mark.parametrize("L", [64, 128, 256, 512, 1024, 2048, 4096, 8192])
+def test_dimwise_matches_the_reference_python_model(L):
+    W, P, C = oracle.DIMWISE_GEOMETRY[L]
+    G = W * C
+    rng = np.random.default_rng(L)
+    B, D = 2, 3
+    a = 0.99 + 0.01 * rng.random((B, D, L))  # scans/contraction_scan.py:154-159 distributions
+    x = rng.standard_normal((B, D, L)) / G
+    bh = rng.standard_normal((B, D, G)) / G
+    wq = 0.01 * rng.random(D)
+    wk = 0.01 * rng.random(D)
+    got = oracle.dimwise_f64(a, x, bh, wq, wk)
+    kbh = torch.tensor(((1 + wk)[None, :, None] * bh[:, :, :W]).transpose(0, 2, 1))
+    want = _contraction_model(torch.tensor(a.transpose(0, 2, 1)),
+                              torch.tensor(x.transpose(0, 2, 1)), kbh,
+                              torch.tensor(1 + wq)[None, None, :], G, C)
+    np.testing.assert_allclose(got, want.numpy().transpose(0, 2, 1), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("L", [64, 512, 4096, 16384])
+def test_dimwise_closed_form_with_unit_gates_and_zero_keys(L):
+    """Gates 1, k = 0: every score is 0 > -1e10, so m = 0 and r[g] = v[g]. Then each group
+    is its own cumsum (group 0 from the chunk carry) plus the previous group's total."""
+    W, P, C = oracle.DIMWISE_GEOMETRY[L]
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 3, L))
+    ones = np.ones_like(x)
+    got = oracle.dimwise_f64(ones, x, np.zeros((2, 3, W * C)), np.zeros(3), np.zeros(3))
+    want = np.empty_like(x)
+    carry = np.zeros((2, 3))
+    for c in range(C):
+        cs = np.cumsum(x[:, :, c * W * P:(c + 1) * W * P].reshape(2, 3, W, P), axis=-1)
+        cs[:, :, 0] += carry[..., None]
+        totals = cs[..., -1].copy()
+        cs[:, :, 1:] += totals[:, :, :-1, None]
+        want[:, :, c * W * P:(c + 1) * W * P] = cs.reshape(2, 3, W * P)
+        carry = cs[:, :, -1, -1]
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_dimwise_two_groups_is_a_cumsum():
+    """seqlen 64: two groups and no selection, so with gates 1 the output is cumsum(x)."""
+    x = np.random.default_rng(4).standard_normal((1, 2, 64))
+    got = oracle.dimwise_f64(np.ones_like(x), x, np.ones((1, 2, 2)), np.zeros(2), np.zeros(2))
+    np.testing.assert_allclose(got, np.cumsum(x, axis=-1), rtol=1e-12, atol=1e-12)
+
+
+def test_dimwise_ties_pick_the_first_group():
+    """Equal keys and q > 0: all scores tie, the first strict maximum is group 0, so
+    r[g] = (k q[g]) v[0] + v[g] with q[g] = v[g]."""
+    L = 1024
+    W, P, _ = oracle.DIMWISE_GEOMETRY[L]
+    x = 0.5 + np.random.default_rng(5).random((1, 1, L))  # positive: v > 0
+    k = 0.25
+    got = oracle.dimwise_f64(np.ones_like(x), x, np.full((1, 1, W), k), np.zeros(1), np.zeros(1))
+    cs = np.cumsum(x.reshape(W, P), axis=-1)
+    v = cs[:, -1]
+    r = v.copy()
+    r[1:W - 1] = (k * v[1:W - 1]) * v[0] + v[1:W - 1]
+    cs[1:] += r[:-1, None]
+    np.testing.assert_allclose(got.reshape(W, P), cs, rtol=1e-12, atol=1e-12)
