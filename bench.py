@@ -365,6 +365,46 @@ def bench_channel_last(args):
     return entry
 
 
+def bench_fused(args):
+    """c4fused: the Mamba-style step with the gate producer fused in, at the headline shape.
+    Fused: pscan_softplus(z, rate, x) forward + backward (reads z, x, writes y; reads z, y,
+    grad_out, writes grad_z, grad_x: 8 N s bytes). Unfused, for comparison: torch computes
+    gates = exp(-softplus(z) * rate) and autograd runs pscan and the producer's backward."""
+    import fpscan_amd
+
+    B, D, L = 8, 1024, 65536
+    dtype = DTYPES[args.dtype or "bfloat16"]
+    s = torch.empty((), dtype=dtype).element_size()
+    N = B * D * L
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    z = torch.randn(B, D, L, generator=gen, device="cuda").to(dtype).requires_grad_()
+    rate = (0.001 + 0.099 * torch.rand(D, generator=gen, device="cuda")).requires_grad_()
+    x = (0.1 * torch.randn(B, D, L, generator=gen, device="cuda")).to(dtype).requires_grad_()
+    go = torch.randn(B, D, L, generator=gen, device="cuda").to(dtype)
+
+    def fused():
+        y = fpscan_amd.pscan_softplus(z, rate, x)
+        return torch.autograd.grad(y, (z, rate, x), go)
+
+    def unfused():
+        gates = torch.exp(-torch.nn.functional.softplus(z) * rate[None, :, None].to(dtype))
+        y = fpscan_amd.pscan(gates, x)
+        return torch.autograd.grad(y, (z, rate, x), go)
+
+    res = {"workload": "c4fused: softplus-gate scan fwd+bwd B8 D1024 L65536",
+           "dtype": SHORT[dtype]}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        t = time_each(fn, 3, args.iters)
+        p50 = percentile(t, 0.5)
+        res[name] = {"p50_ms": round(p50, 5)}
+    p50 = res["fused"]["p50_ms"]
+    res["fused"]["gbps"] = round(8 * N * s / (p50 / 1e3) / 1e9, 1)
+    res["fused"]["hbm_frac"] = round(8 * N * s / (p50 / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)
+    res["speedup_vs_unfused"] = round(res["unfused"]["p50_ms"] / p50, 3)
+    print(json.dumps(res), flush=True)
+    return res
+
+
 def bench_dimwise(args):
     """dw: dimwise_forward (the reference module's contraction scan) at the headline shape,
     B8 D1024 L65536; 3 N s bytes per call (read Ax and Bx, write Bx; Bh, Wq, Wk are
@@ -398,7 +438,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw"])
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw", "c4fused"])
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -439,6 +479,8 @@ def main():
         res = bench_channel_last(args)
     elif args.workload == "dw":
         res = bench_dimwise(args)
+    elif args.workload == "c4fused":
+        res = bench_fused(args)
     else:
         res = bench_shape(args)
     print(json.dumps(res), flush=True)

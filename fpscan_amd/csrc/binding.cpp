@@ -9,7 +9,7 @@
 // Added: `fullscan_backward`, the fused backward that replaces the composition in
 // fpscan/ops.py:69-83, plus the checks the reference leaves out (shapes, `out`, device);
 // `fullscan_forward_cl` / `fullscan_backward_cl` for (batch, seqlen, dim) tensors;
-// `dimwise_forward` (csrc/main.cpp:10), the contraction scan.
+// `dimwise_forward` (csrc/main.cpp:10), the contraction scan; the fused softplus-gate scan.
 // Every check runs before any HIP call, so a bad call raises RuntimeError on any machine.
 #include <torch/extension.h>
 
@@ -254,6 +254,78 @@ void dimwise_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tenso
   check_status(status);
 }
 
+// ---- fused softplus gates: gates = exp(-softplus(z) * rate[d]) computed inside the scan (no
+// reference counterpart: the reference takes materialised gates). rate: fp32, one per dim.
+void check_rate(const at::Tensor& rate, const at::Tensor& like, const char* name) {
+  TORCH_CHECK(rate.device() == like.device(), name, " must be on ", like.device());
+  TORCH_CHECK(rate.scalar_type() == at::kFloat, name, " must be float32, got ",
+              rate.scalar_type());
+  TORCH_CHECK(rate.is_contiguous() && rate.numel() == like.size(1), name, " must be a contiguous",
+              " float32 tensor with one value per dim (", like.size(1), "), got ", rate.sizes());
+}
+
+at::Tensor fullscan_forward_softplus(const at::Tensor& z, const at::Tensor& rate,
+                                     const at::Tensor& tokens, const at::Tensor& out,
+                                     bool reverse) {
+  check_input(z, "z");
+  check_input(tokens, "tokens");
+  check_like(z, tokens, "z", "tokens");
+  check_input(out, "out");
+  check_like(out, tokens, "out", "tokens");
+  check_rate(rate, tokens, "rate");
+  check_seqlen(tokens.size(2));
+  if (tokens.numel() == 0) return out;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(tokens.device());
+  void* stream =
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(tokens.device().index()).stream();
+  const int64_t D = tokens.size(1), L = tokens.size(2);
+  const int status = fpscan_scan_fwd_softplus(
+      z.data_ptr(), rate.data_ptr<float>(), tokens.data_ptr(), out.data_ptr(), tokens.size(0),
+      D, L, D * L, L, dtype_code(tokens.scalar_type()), reverse ? 1 : 0, stream);
+  check_status(status);
+  return out;
+}
+
+void fullscan_backward_softplus(const at::Tensor& z, const at::Tensor& rate,
+                                const at::Tensor& out, const at::Tensor& grad_out,
+                                const at::Tensor& grad_z, const at::Tensor& grad_tokens,
+                                const at::Tensor& grad_rate_rows) {
+  check_input(z, "z");
+  check_input(out, "out");
+  check_input(grad_out, "grad_out");
+  check_input(grad_z, "grad_z");
+  check_input(grad_tokens, "grad_tokens");
+  check_like(out, z, "out", "z");
+  check_like(grad_out, z, "grad_out", "z");
+  check_like(grad_z, z, "grad_z", "z");
+  check_like(grad_tokens, z, "grad_tokens", "z");
+  check_rate(rate, z, "rate");
+  check_seqlen(z.size(2));
+  const int64_t rows = z.size(0) * z.size(1);
+  TORCH_CHECK(grad_rate_rows.device() == z.device() &&
+                  grad_rate_rows.scalar_type() == at::kFloat &&
+                  grad_rate_rows.is_contiguous() && grad_rate_rows.numel() == rows,
+              "grad_rate_rows must be a contiguous float32 tensor with batch*dim (", rows,
+              ") elements");
+  if (z.numel() == 0) return;
+  for (const at::Tensor* o : {&grad_z, &grad_tokens}) {
+    for (const at::Tensor* i : {&z, &out, &grad_out}) {
+      TORCH_CHECK(o->data_ptr() != i->data_ptr(), "fullscan_backward_softplus outputs must not "
+                  "alias its inputs");
+    }
+  }
+  TORCH_CHECK(grad_z.data_ptr() != grad_tokens.data_ptr(),
+              "grad_z and grad_tokens must be distinct");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(z.device());
+  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(z.device().index()).stream();
+  const int64_t D = z.size(1), L = z.size(2);
+  const int status = fpscan_scan_bwd_softplus(
+      z.data_ptr(), rate.data_ptr<float>(), out.data_ptr(), grad_out.data_ptr(),
+      grad_z.data_ptr(), grad_tokens.data_ptr(), grad_rate_rows.data_ptr<float>(), z.size(0), D,
+      L, D * L, L, dtype_code(z.scalar_type()), stream);
+  check_status(status);
+}
+
 int set_launch_override(int waves_per_row, int ring_depth) {
   const int status = fpscan_set_launch_override(waves_per_row, ring_depth);
   TORCH_CHECK(status == FPSCAN_OK, "waves_per_row must be one of 0,1,2,4,8,16 and ring_depth "
@@ -278,6 +350,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "fused backward of the channel-last forward scan: (grad_gates, grad_tokens)",
         pybind11::arg("gates"), pybind11::arg("out"), pybind11::arg("grad_out"),
         pybind11::arg("grad_gates"), pybind11::arg("grad_tokens"));
+  m.def("fullscan_forward_softplus", &fullscan_forward_softplus,
+        "scan with gates exp(-softplus(z) * rate[d]) computed on load, written into out",
+        pybind11::arg("z"), pybind11::arg("rate"), pybind11::arg("tokens"), pybind11::arg("out"),
+        pybind11::arg("reverse"));
+  m.def("fullscan_backward_softplus", &fullscan_backward_softplus,
+        "fused backward of the softplus-gate scan: writes grad_z, grad_tokens and one "
+        "d loss / d rate partial per row", pybind11::arg("z"), pybind11::arg("rate"),
+        pybind11::arg("out"), pybind11::arg("grad_out"), pybind11::arg("grad_z"),
+        pybind11::arg("grad_tokens"), pybind11::arg("grad_rate_rows"));
   m.def("dimwise_forward", &dimwise_forward,
         "contraction scan, in place into Bx (HIP, gfx950)", pybind11::arg("Ax"),
         pybind11::arg("Bx"), pybind11::arg("Bh"), pybind11::arg("Wq"), pybind11::arg("Wk"));

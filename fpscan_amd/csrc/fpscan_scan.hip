@@ -56,6 +56,10 @@ struct Args {
   int64_t stride_d;
   int32_t seqlen;
   int32_t contiguous;
+  // fused softplus gates only: per-channel rate (dim floats) and, for the backward, one
+  // partial sum of d loss / d rate per row (rows floats, may be null)
+  const float* rate;
+  float* grad_rate_rows;
 };
 
 
@@ -117,20 +121,75 @@ __device__ __forceinline__ void load_slot(const RowRsrc<kMode>& rr, Slot<kMode>&
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Gate producers. GatePlain: the gates tensor holds the gates. GateSoftplus: it holds z, and
+// the gate is exp(-softplus(z) * rate[d]) -- a Mamba-style decay (delta = softplus(z),
+// A = -rate) -- computed on load, so the gates never exist in memory.
+// ---------------------------------------------------------------------------------------
+struct GatePlain {
+  static constexpr bool kFused = false;
+  template <int V>
+  struct Aux {};
+  __device__ static __forceinline__ float gate(float g, float) { return g; }
+};
+
+struct GateSoftplus {
+  static constexpr bool kFused = true;
+  // per element, memory order: d gate / d z and d gate / d rate, for the backward
+  template <int V>
+  struct Aux {
+    float dz[V];
+    float dr[V];
+  };
+  // softplus(z) = max(z, 0) + log1p(t), t = exp(-|z|) in (0, 1]. log1p(t) by Goldberg's
+  // rule: w = 1 + t, log1p(t) = t if w == 1 else log(w) * t / (w - 1) (D. Goldberg, "What
+  // every computer scientist should know about floating-point arithmetic", 1991, thm. 4),
+  // which stays accurate for small t. exp and log through the hardware's base-2
+  // instructions; sigmoid(z) = 1/w (z >= 0) or t/w.
+  __device__ static __forceinline__ void eval(float z, float rate, float& gate, float& dz,
+                                              float& dr) {
+    constexpr float kLog2e = 1.4426950408889634f;
+    constexpr float kLn2 = 0.6931471805599453f;
+    const float t = __builtin_amdgcn_exp2f(-fabsf(z) * kLog2e);
+    const float w = 1.0f + t;
+    const float rw = __builtin_amdgcn_rcpf(w);
+    const float l1p = (w == 1.0f) ? t
+                                  : __builtin_amdgcn_logf(w) * kLn2 * t *
+                                        __builtin_amdgcn_rcpf(w - 1.0f);
+    const float sp = fmaxf(z, 0.0f) + l1p;
+    gate = __builtin_amdgcn_exp2f(-sp * rate * kLog2e);
+    const float sig = (z >= 0.0f) ? rw : t * rw;
+    dz = -gate * rate * sig;
+    dr = -gate * sp;
+  }
+  __device__ static __forceinline__ float gate(float z, float rate) {
+    float g, dz, dr;
+    eval(z, rate, g, dz, dr);
+    return g;
+  }
+};
+
 // Builds the per-lane affine maps (alpha, beta) in processing order from a loaded slot.
 // For the backward also returns y[t-1] per element (processing order) in ysh.
 // `gate_next`/`out_prev` are the neighbour values for the lanes at the edges of the span
 // (uniform boundary values for long rows, the identity for short-row segments);
 // `span_first_lane`/`span_last_lane` say whether this lane is the first/last lane of its
 // span in processing order.
-template <class E, int kMode>
+template <class E, int kMode, class Gp = GatePlain>
 __device__ __forceinline__ void make_maps(const Slot<kMode>& s, float (&al)[E::V], float (&be)[E::V],
                                           float (&ysh)[E::V], float gate_next, float out_prev,
-                                          bool span_first_lane, bool span_last_lane) {
+                                          bool span_first_lane, bool span_last_lane,
+                                          float rate = 0.0f,
+                                          typename Gp::template Aux<E::V>* aux = nullptr) {
   constexpr int V = E::V;
   float g[V], x[V];
   E::unpack(s.v[0], g);
   E::unpack(s.v[1], x);
+  if constexpr (Gp::kFused) {
+    // z -> gates (memory order); `gate_next` arrives already converted
+#pragma unroll
+    for (int e = 0; e < V; ++e) Gp::eval(g[e], rate, g[e], aux->dz[e], aux->dr[e]);
+  }
   if constexpr (kMode == kBwd) {
     float y[V];
     E::unpack(s.v[2], y);
@@ -174,10 +233,12 @@ __device__ __forceinline__ void lane_aggregate(const float (&al)[E::V], const fl
 
 // Re-runs the lane's elements from the value entering the lane; returns the packed output
 // vector(s) in memory order (o1 only for the backward: grad_gates).
-template <class E, int kMode>
+template <class E, int kMode, class Gp = GatePlain>
 __device__ __forceinline__ void finish_lane(const float (&al)[E::V], const float (&be)[E::V],
                                             const float (&ysh)[E::V], float y, u32x4& o0,
-                                            u32x4& o1) {
+                                            u32x4& o1,
+                                            const typename Gp::template Aux<E::V>* aux = nullptr,
+                                            float* rate_sum = nullptr) {
   constexpr int V = E::V;
   float res[V];
 #pragma unroll
@@ -193,14 +254,55 @@ __device__ __forceinline__ void finish_lane(const float (&al)[E::V], const float
     float gg[V];
 #pragma unroll
     for (int e = 0; e < V; ++e) gg[e] = om[e] * ysh[V - 1 - e];
+    if constexpr (Gp::kFused) {
+      // d loss / d gate -> d loss / d z (written) and d loss / d rate (summed per row)
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        *rate_sum = fmaf(gg[e], aux->dr[e], *rate_sum);
+        gg[e] *= aux->dz[e];
+      }
+    }
     o1 = E::pack(gg);
   }
+}
+
+// Sums of one value over the wave (result in every lane) and over aligned segments of G
+// lanes (inclusive: the segment's last lane holds its total).
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kRowShr1>(0.0f, v);
+  v += dpp<kRowShr2>(0.0f, v);
+  v += dpp<kRowShr4>(0.0f, v);
+  v += dpp<kRowShr8>(0.0f, v);
+  v += dpp<kRowBcast15, 0xa>(0.0f, v);
+  v += dpp<kRowBcast31, 0xc>(0.0f, v);
+  return readlane(v, 63);
+}
+
+template <int G>
+__device__ __forceinline__ float segment_sum(float v, int sl) {
+  if constexpr (G >= 16) {
+    v += dpp<kRowShr1>(0.0f, v);
+    v += dpp<kRowShr2>(0.0f, v);
+    v += dpp<kRowShr4>(0.0f, v);
+    v += dpp<kRowShr8>(0.0f, v);
+    if constexpr (G == 32) v += dpp<kRowBcast15, 0xa>(0.0f, v);
+  } else {
+    float s = dpp<kRowShr1>(0.0f, v);
+    v += sl >= 1 ? s : 0.0f;
+    s = dpp<kRowShr2>(0.0f, v);
+    v += sl >= 2 ? s : 0.0f;
+    if constexpr (G == 8) {
+      s = dpp<kRowShr4>(0.0f, v);
+      v += sl >= 4 ? s : 0.0f;
+    }
+  }
+  return v;
 }
 
 // ---------------------------------------------------------------------------------------
 // Long rows: W waves per row, U sub-chunks in flight per wave.
 // ---------------------------------------------------------------------------------------
-template <class E, int kMode, int W, int U>
+template <class E, int kMode, int W, int U, class Gp = GatePlain>
 __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Args a) {
   constexpr int V = E::V;
   constexpr int kSub = 64 * V;
@@ -208,6 +310,7 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
   constexpr int kRowsPerBlock = (W == 1) ? 4 : 1;
 
   __shared__ f32x2 exch[2][W];
+  __shared__ float rate_part[W];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -231,6 +334,8 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
       rr.in2 = row_rsrc(a.in2, base, E::kSize, row_bytes);
       rr.out1 = row_rsrc(a.out1, base, E::kSize, row_bytes);
     }
+    float rate = 0.0f, rate_sum = 0.0f;
+    if constexpr (Gp::kFused) rate = a.rate[row % a.dim];
 
     // byte offset inside the row of the sub-chunk this wave handles in round r
     auto sub_bytes = [&](int r) -> uint32_t {
@@ -254,11 +359,15 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         float gate_next = 1.0f, out_prev = 0.0f;
         if constexpr (kMode == kBwd) {
           // identity at the row edges: gates[L] = 1, y[-1] = 0
-          gate_next = (sb + kSub * E::kSize < (uint32_t)row_bytes) ? ring[u].gate_after : 1.0f;
+          gate_next = (sb + kSub * E::kSize < (uint32_t)row_bytes)
+                          ? Gp::gate(ring[u].gate_after, rate)
+                          : 1.0f;
           out_prev = (sb > 0) ? ring[u].out_before : 0.0f;
         }
         float al[V], be[V], ysh[V];
-        make_maps<E, kMode>(ring[u], al, be, ysh, gate_next, out_prev, lane == 0, lane == 63);
+        typename Gp::template Aux<V> aux;
+        make_maps<E, kMode, Gp>(ring[u], al, be, ysh, gate_next, out_prev, lane == 0, lane == 63,
+                                rate, &aux);
         if (kMode != kBwd && r == 0 && w == 0 && lane == 0) {
           // the first element of the row in processing order never uses its gate
           // (gates[0] forward, gates[L-1] reverse), as in full_scan.cu:96
@@ -290,7 +399,7 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         const float y_lane_end = fmaf(A, c_in, B);
         const float y_enter = dpp<kWaveShr1>(c_in, y_lane_end);
         u32x4 o0, o1;
-        finish_lane<E, kMode>(al, be, ysh, y_enter, o0, o1);
+        finish_lane<E, kMode, Gp>(al, be, ysh, y_enter, o0, o1, &aux, &rate_sum);
         bst16(rr.out0, sb + lane_off, o0);
         if constexpr (kMode == kBwd) bst16(rr.out1, sb + lane_off, o1);
         const uint32_t next = (r + U < nrounds) ? sub_bytes(r + U) : kNoOffset;
@@ -298,6 +407,22 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         // keep the ring order: without this the scheduler hoists the next slot's arithmetic
         // above this slot's refill, which turns every wait into a wait for all loads
         __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if constexpr (Gp::kFused && kMode == kBwd) {
+      // d loss / d rate of this row: lanes, then waves in order (deterministic)
+      const float s = wave_sum(rate_sum);
+      if constexpr (W == 1) {
+        if (a.grad_rate_rows != nullptr && lane == 0) a.grad_rate_rows[row] = s;
+      } else {
+        if (lane == 0) rate_part[w] = s;
+        lds_barrier();
+        if (w == 0 && lane == 0 && a.grad_rate_rows != nullptr) {
+          float tot = 0.0f;
+          for (int i = 0; i < W; ++i) tot += rate_part[i];
+          a.grad_rate_rows[row] = tot;
+        }
+        lds_barrier();  // rate_part is rewritten by the next row
       }
     }
   }
@@ -708,7 +833,7 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
 // ---------------------------------------------------------------------------------------
 // Short rows: G lanes per row (seqlen = G * V), 64/G rows per wave, 4 waves per block.
 // ---------------------------------------------------------------------------------------
-template <class E, int kMode, int G>
+template <class E, int kMode, int G, class Gp = GatePlain>
 __global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
   constexpr int V = E::V;
   constexpr bool kReverse = kMode != kFwd;
@@ -739,8 +864,11 @@ __global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
 #pragma unroll
       for (int i = 0; i < (kMode == kBwd ? 3 : 2); ++i) s.v[i] = u32x4{0u, 0u, 0u, 0u};
     }
+    float rate = 0.0f, rate_sum = 0.0f;
+    if constexpr (Gp::kFused) rate = valid ? a.rate[row % a.dim] : 0.0f;
     float al[V], be[V], ysh[V];
-    make_maps<E, kMode>(s, al, be, ysh, 1.0f, 0.0f, sl == 0, sl == G - 1);
+    typename Gp::template Aux<V> aux;
+    make_maps<E, kMode, Gp>(s, al, be, ysh, 1.0f, 0.0f, sl == 0, sl == G - 1, rate, &aux);
     if (kMode != kBwd && sl == 0) al[0] = 1.0f;
     float A, B;
     lane_aggregate<E>(al, be, A, B);
@@ -748,10 +876,14 @@ __global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
     float y_enter = dpp<kWaveShr1>(0.0f, B);
     y_enter = (sl == 0) ? 0.0f : y_enter;
     u32x4 o0, o1;
-    finish_lane<E, kMode>(al, be, ysh, y_enter, o0, o1);
+    finish_lane<E, kMode, Gp>(al, be, ysh, y_enter, o0, o1, &aux, &rate_sum);
     if (valid) {
       st16(a.out0, base + (int64_t)vec * V, E::kSize, o0);
       if constexpr (kMode == kBwd) st16(a.out1, base + (int64_t)vec * V, E::kSize, o1);
+    }
+    if constexpr (Gp::kFused && kMode == kBwd) {
+      const float tot = segment_sum<G>(rate_sum, sl);  // the row's last lane holds its sum
+      if (valid && sl == G - 1 && a.grad_rate_rows != nullptr) a.grad_rate_rows[row] = tot;
     }
   }
 }
@@ -833,35 +965,35 @@ int launch(const void* kernel, int64_t groups, int threads, const Args& a, hipSt
   return err == hipSuccess ? FPSCAN_OK : FPSCAN_ERR_LAUNCH;
 }
 
-template <class E, int kMode, int W>
+template <class E, int kMode, int W, class Gp>
 const void* long_kernel(int u) {
   if constexpr (W == 1) {
-    if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4>);
+    if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4, Gp>);
   }
   // W > 1 keeps at most two sub-chunks in flight per wave: the W waves of a row already
   // multiply the bytes in flight, and deeper rings exceed 64 VGPRs.
-  if (u >= 2) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 2>);
-  return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 1>);
+  if (u >= 2) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 2, Gp>);
+  return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 1, Gp>);
 }
 
-template <class E, int kMode>
+template <class E, int kMode, class Gp>
 const void* long_kernel(int w, int u) {
   switch (w) {
-    case 1: return long_kernel<E, kMode, 1>(u);
-    case 2: return long_kernel<E, kMode, 2>(u);
-    case 4: return long_kernel<E, kMode, 4>(u);
-    case 8: return long_kernel<E, kMode, 8>(u);
-    default: return long_kernel<E, kMode, 16>(u);
+    case 1: return long_kernel<E, kMode, 1, Gp>(u);
+    case 2: return long_kernel<E, kMode, 2, Gp>(u);
+    case 4: return long_kernel<E, kMode, 4, Gp>(u);
+    case 8: return long_kernel<E, kMode, 8, Gp>(u);
+    default: return long_kernel<E, kMode, 16, Gp>(u);
   }
 }
 
-template <class E, int kMode>
+template <class E, int kMode, class Gp>
 const void* short_kernel(int g) {
   switch (g) {
-    case 4: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 4>);
-    case 8: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 8>);
-    case 16: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 16>);
-    default: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 32>);
+    case 4: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 4, Gp>);
+    case 8: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 8, Gp>);
+    case 16: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 16, Gp>);
+    default: return reinterpret_cast<const void*>(&scan_short_rows<E, kMode, 32, Gp>);
   }
 }
 
@@ -896,14 +1028,16 @@ int run_tiled(const Args& a, const TilePlan& plan, void* workspace, hipStream_t 
   return err == hipSuccess ? FPSCAN_OK : FPSCAN_ERR_LAUNCH;
 }
 
-template <class E, int kMode>
+// Fused-gate calls (Gp = GateSoftplus) always stream rows: the tiled kernel rebuilds a tile's
+// maps at its deferred finish, which would evaluate the gate transform twice.
+template <class E, int kMode, class Gp = GatePlain>
 int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   constexpr int V = E::V;
   constexpr int kSub = 64 * V;
   const int L = a.seqlen;
   const TilePlan plan =
       plan_tiles(a.rows, L, E::kSize, g_tiling.load(std::memory_order_relaxed));
-  if (plan.use && workspace != nullptr && ws_bytes >= plan.bytes) {
+  if (!Gp::kFused && plan.use && workspace != nullptr && ws_bytes >= plan.bytes) {
     const int st = run_tiled<E, kMode>(a, plan, workspace, stream,
                                        E::kSlot * 3 + kMode);
     if (st >= 0) return st;
@@ -911,7 +1045,7 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (L < kSub) {
     const int g = L / V;
     const int64_t rows_per_block = 4 * (64 / g);
-    return launch(short_kernel<E, kMode>(g), (a.rows + rows_per_block - 1) / rows_per_block,
+    return launch(short_kernel<E, kMode, Gp>(g), (a.rows + rows_per_block - 1) / rows_per_block,
                   256, a, stream);
   }
   const int nsub = L / kSub;
@@ -927,16 +1061,16 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (ou > 0) u_max = ou;
   const int nrounds = nsub / w;
   const int u = u_max < nrounds ? u_max : nrounds;
-  if (w == 1) return launch(long_kernel<E, kMode>(1, u), (a.rows + 3) / 4, 256, a, stream);
-  return launch(long_kernel<E, kMode>(w, u), a.rows, 64 * w, a, stream);
+  if (w == 1) return launch(long_kernel<E, kMode, Gp>(1, u), (a.rows + 3) / 4, 256, a, stream);
+  return launch(long_kernel<E, kMode, Gp>(w, u), a.rows, 64 * w, a, stream);
 }
 
-template <int kMode>
+template <int kMode, class Gp = GatePlain>
 int dispatch(int dtype, const Args& a, void* ws, size_t ws_bytes, hipStream_t stream) {
   switch (dtype) {
-    case FPSCAN_DTYPE_F32: return run<F32, kMode>(a, ws, ws_bytes, stream);
-    case FPSCAN_DTYPE_F16: return run<F16, kMode>(a, ws, ws_bytes, stream);
-    case FPSCAN_DTYPE_BF16: return run<BF16, kMode>(a, ws, ws_bytes, stream);
+    case FPSCAN_DTYPE_F32: return run<F32, kMode, Gp>(a, ws, ws_bytes, stream);
+    case FPSCAN_DTYPE_F16: return run<F16, kMode, Gp>(a, ws, ws_bytes, stream);
+    case FPSCAN_DTYPE_BF16: return run<BF16, kMode, Gp>(a, ws, ws_bytes, stream);
     default: return FPSCAN_ERR_DTYPE;
   }
 }
@@ -1015,6 +1149,49 @@ int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out, vo
   a.out0 = grad_tokens;
   a.out1 = grad_gates;
   return dispatch<kBwd>(dtype, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int fpscan_scan_fwd_softplus(const void* z, const float* rate, const void* tokens, void* out,
+                             int64_t batch, int64_t dim, int64_t seqlen, int64_t stride_b,
+                             int64_t stride_d, int dtype, int reverse, void* stream) {
+  Args a{};
+  const int st = validate(batch, dim, seqlen, stride_b, stride_d, dtype, &a);
+  if (st != FPSCAN_OK) return st;
+  if (a.rows == 0) return FPSCAN_OK;
+  if (!z || !rate || !tokens || !out) return FPSCAN_ERR_NULL;
+  if (!aligned16(z) || !aligned16(tokens) || !aligned16(out) ||
+      (reinterpret_cast<uintptr_t>(rate) & 3u) != 0)
+    return FPSCAN_ERR_ALIGN;
+  a.in0 = z;
+  a.in1 = tokens;
+  a.out0 = out;
+  a.rate = rate;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return reverse ? dispatch<kRev, GateSoftplus>(dtype, a, nullptr, 0, s)
+                 : dispatch<kFwd, GateSoftplus>(dtype, a, nullptr, 0, s);
+}
+
+int fpscan_scan_bwd_softplus(const void* z, const float* rate, const void* out,
+                             const void* grad_out, void* grad_z, void* grad_tokens,
+                             float* grad_rate_rows, int64_t batch, int64_t dim, int64_t seqlen,
+                             int64_t stride_b, int64_t stride_d, int dtype, void* stream) {
+  Args a{};
+  const int st = validate(batch, dim, seqlen, stride_b, stride_d, dtype, &a);
+  if (st != FPSCAN_OK) return st;
+  if (a.rows == 0) return FPSCAN_OK;
+  if (!z || !rate || !out || !grad_out || !grad_z || !grad_tokens) return FPSCAN_ERR_NULL;
+  if (!aligned16(z) || !aligned16(out) || !aligned16(grad_out) || !aligned16(grad_z) ||
+      !aligned16(grad_tokens) || (reinterpret_cast<uintptr_t>(rate) & 3u) != 0 ||
+      (reinterpret_cast<uintptr_t>(grad_rate_rows) & 3u) != 0)
+    return FPSCAN_ERR_ALIGN;
+  a.in0 = z;
+  a.in1 = grad_out;
+  a.in2 = out;
+  a.out0 = grad_tokens;
+  a.out1 = grad_z;
+  a.rate = rate;
+  a.grad_rate_rows = grad_rate_rows;
+  return dispatch<kBwd, GateSoftplus>(dtype, a, nullptr, 0, static_cast<hipStream_t>(stream));
 }
 
 size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype, int op) {

@@ -21,7 +21,8 @@ from typing import Optional, Tuple
 import torch
 
 __all__ = ["pscan", "scan_forward", "scan_backward", "PScan", "pscan_channel_last",
-           "scan_forward_channel_last", "scan_backward_channel_last", "PScanChannelLast"]
+           "scan_forward_channel_last", "scan_backward_channel_last", "PScanChannelLast",
+           "pscan_softplus", "scan_forward_softplus", "scan_backward_softplus", "PScanSoftplus"]
 
 _EXT_CANDIDATES = ("fpscan_amd._C",)
 _ext = None
@@ -167,6 +168,68 @@ class PScanChannelLast(torch.autograd.Function):
 def pscan_channel_last(gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
     """Differentiable scan of (batch, seqlen, dim) tensors along seqlen."""
     return PScanChannelLast.apply(gates, tokens)
+
+
+# ---------------------------------------------------------------------------------------
+# Fused gate producer: gates = exp(-softplus(z) * rate[d]) (a Mamba-style decay:
+# delta = softplus(z), A = -rate) computed inside the scan, so the gates tensor is never
+# written or read. No reference counterpart; it replaces "compute gates, then pscan".
+# ---------------------------------------------------------------------------------------
+def scan_forward_softplus(
+    z: torch.Tensor,
+    rate: torch.Tensor,
+    tokens: torch.Tensor,
+    reverse: bool = False,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """``scan_forward(torch.exp(-softplus(z) * rate[:, None]), tokens, reverse)`` without the
+    gates tensor. z, tokens: (batch, dim, seqlen) contiguous of one dtype; rate: float32,
+    one value per dim."""
+    ext = _load_extension()
+    if out is None:
+        out = torch.empty_like(tokens)
+    ext.fullscan_forward_softplus(z, rate, tokens, out, reverse)
+    return out
+
+
+def scan_backward_softplus(
+    z: torch.Tensor,
+    rate: torch.Tensor,
+    out: torch.Tensor,
+    grad_out: torch.Tensor,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(grad_z, grad_rate, grad_tokens) of ``scan_forward_softplus`` (forward direction)
+    given its output. grad_rate is float32 with rate's shape: the kernel writes one partial
+    sum per (batch, dim) row and the batch is summed here."""
+    ext = _load_extension()
+    grad_z = torch.empty_like(z)
+    grad_tokens = torch.empty_like(z)
+    B, D = z.shape[0], z.shape[1]
+    rows = torch.empty(B * D, dtype=torch.float32, device=z.device)
+    ext.fullscan_backward_softplus(z, rate, out, grad_out, grad_z, grad_tokens, rows)
+    return grad_z, rows.view(B, D).sum(0).view(rate.shape), grad_tokens
+
+
+class PScanSoftplus(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, z: torch.Tensor, rate: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+        out = scan_forward_softplus(z, rate, tokens)
+        ctx.save_for_backward(z, rate, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        z, rate, out = ctx.saved_tensors
+        grad_z, grad_rate, grad_tokens = scan_backward_softplus(z, rate, out,
+                                                                grad_output.contiguous())
+        return grad_z, grad_rate, grad_tokens
+
+
+def pscan_softplus(z: torch.Tensor, rate: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """Differentiable ``pscan(torch.exp(-softplus(z) * rate[:, None]), tokens)`` with the
+    gates computed inside the kernels (forward and backward)."""
+    return PScanSoftplus.apply(z, rate, tokens)
 
 
 # ---------------------------------------------------------------------------------------

@@ -130,6 +130,28 @@ int fpscan_scan_bwd_cl(const void* gates, const void* out, const void* grad_out,
 size_t fpscan_workspace_bytes_cl(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_t,
                                  int dtype, int op);
 
+/* Scan with the gates produced inside the kernel: gates[b,d,t] = exp(-softplus(z[b,d,t]) *
+ * rate[d]) (a Mamba-style decay, delta = softplus(z), A = -rate), so that the gates tensor is
+ * never written or read: 3 N s bytes for the forward instead of 5 N s for "compute gates,
+ * then scan". z and tokens as `gates`/`tokens` of fpscan_scan_fwd; rate: fp32, `dim` values,
+ * 4-byte aligned. Always takes the row-streaming path (no workspace). No reference
+ * counterpart (the reference scans materialised gates). */
+int fpscan_scan_fwd_softplus(const void* z, const float* rate, const void* tokens, void* out,
+                             int64_t batch, int64_t dim, int64_t seqlen,
+                             int64_t stride_b, int64_t stride_d,
+                             int dtype, int reverse, void* stream);
+
+/* Fused backward of fpscan_scan_fwd_softplus (forward direction), given its output `out`:
+ * grad_tokens as fpscan_scan_bwd; grad_z = grad_gates * gate * (-rate) * sigmoid(z); and, if
+ * grad_rate_rows is not NULL, one fp32 partial sum of grad_gates * gate * (-softplus(z)) per
+ * (b, d) row (batch * dim floats, index b * dim + d; summing over b gives d loss / d rate). */
+int fpscan_scan_bwd_softplus(const void* z, const float* rate, const void* out,
+                             const void* grad_out, void* grad_z, void* grad_tokens,
+                             float* grad_rate_rows,
+                             int64_t batch, int64_t dim, int64_t seqlen,
+                             int64_t stride_b, int64_t stride_d,
+                             int dtype, void* stream);
+
 /* Contraction scan, in place into `tokens` (the reference's Bx):
  * replaces dimwise_forward / dimwise_fwd / dimwise_pscan (csrc/main.cpp:10,
  * csrc/dimwise/dimwise.h:27-42, csrc/dimwise/dimwise_scan_final.cu:387-576).

@@ -19,6 +19,9 @@ What each function restates (saeeddhqan/fpscan, paths relative to the reference 
                         op sequence); the CPU baseline bench.py times
   pscan_backward_composed  fpscan/ops.py:69-83: the backward composed from a scan function
                         (shifted gates, reverse scan, shifted output, product)
+  scan_softplus_f64, scan_bwd_softplus_f64
+                        scan_f64 / scan_bwd_f64 with gates exp(-softplus(z) * rate[d]) (the
+                        fused gate producer; no reference counterpart)
   dimwise_f64           csrc/dimwise/dimwise_scan_final.cu:12-576 -- the contraction scan
                         behind dimwise_forward, in float64 (numpy)
   scan_f64_channel_last, scan_bwd_f64_channel_last
@@ -34,7 +37,9 @@ the adjoint identity <go, J v> = <J^T go, v>, and agreement between the two forw
 implementations. ``refkernel_f32`` is pinned against exact results on inputs whose every
 partial result is exactly representable in fp32. The channel-last pair is pinned against a
 direct loop along axis 1, cumsum along axis 1 for g = 1, and float64 autograd through that
-loop. ``dimwise_f64`` is pinned against a restatement of the reference's own Python model of
+loop. The softplus pair is pinned against float64 autograd
+through torch's softplus/exp and a serial loop. ``dimwise_f64`` is pinned against a
+restatement of the reference's own Python model of
 the same computation (scans/contraction_scan.py:98-142, a per-token loop with torch.max for
 the selection), against group-sum closed forms, and on ties.
 """
@@ -157,6 +162,31 @@ def scan_bwd_f64_channel_last(gates, out, grad_out) -> Tuple[np.ndarray, np.ndar
     gg, gx = scan_bwd_f64(sw(gates), sw(out), sw(grad_out))
     return (np.ascontiguousarray(np.swapaxes(gg, -1, -2)),
             np.ascontiguousarray(np.swapaxes(gx, -1, -2)))
+
+
+def softplus_gates_f64(z, rate) -> np.ndarray:
+    """exp(-softplus(z) * rate[d]) in float64 for (batch, dim, seqlen) z and dim rates."""
+    zz = to_f64(z)
+    r = to_f64(rate).reshape(1, zz.shape[1], 1)
+    return np.exp(-np.logaddexp(0.0, zz) * r)
+
+
+def scan_softplus_f64(z, rate, tokens, reverse: bool = False) -> np.ndarray:
+    """``scan_f64`` with the gates made from z and rate (see ``softplus_gates_f64``)."""
+    return scan_f64(softplus_gates_f64(z, rate), tokens, reverse)
+
+
+def scan_bwd_softplus_f64(z, rate, out, grad_out):
+    """(grad_z, grad_rate, grad_tokens) in float64: ``scan_bwd_f64``'s grad_gates carried
+    through gate = exp(-softplus(z) * rate) by the chain rule (d softplus / dz = sigmoid)."""
+    zz = to_f64(z)
+    r = to_f64(rate).reshape(1, zz.shape[1], 1)
+    gates = softplus_gates_f64(zz, rate)
+    gg, gx = scan_bwd_f64(gates, out, grad_out)
+    sig = 0.5 * (1.0 + np.tanh(0.5 * zz))
+    grad_z = gg * gates * (-r) * sig
+    grad_rate = (gg * gates * (-np.logaddexp(0.0, zz))).sum(axis=(0, 2))
+    return grad_z, grad_rate, gx
 
 
 # (W groups per chunk, P elements per group, C chunks) by seqlen: the reference launcher's

@@ -421,3 +421,35 @@ def test_dimwise_ties_pick_the_first_group():
     r[1:W - 1] = (k * v[1:W - 1]) * v[0] + v[1:W - 1]
     cs[1:] += r[:-1, None]
     np.testing.assert_allclose(got.reshape(W, P), cs, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- fused softplus gates
+@pytest.mark.parametrize("shape", [(1, 1, 1), (2, 3, 17), (1, 2, 64)])
+def test_softplus_gate_scan_matches_torch_autograd(shape):
+    """gates = exp(-softplus(z) * rate[d]) through torch's own softplus and exp, a serial
+    loop, and float64 autograd: values and all three gradients."""
+    rng = np.random.default_rng(sum(shape))
+    z = rng.standard_normal(shape) * 3
+    rate = rng.uniform(0.01, 2.0, size=shape[1])
+    x = rng.standard_normal(shape)
+    go = rng.standard_normal(shape)
+    zt = torch.tensor(z, requires_grad=True)
+    rt = torch.tensor(rate, requires_grad=True)
+    xt = torch.tensor(x, requires_grad=True)
+    gates = torch.exp(-torch.nn.functional.softplus(zt) * rt[None, :, None])
+    y = _torch_serial_scan(gates, xt)
+    (y * torch.tensor(go)).sum().backward()
+    want_y = y.detach().numpy()
+    np.testing.assert_allclose(oracle.scan_softplus_f64(z, rate, x), want_y, rtol=1e-12,
+                               atol=1e-12)
+    gz, gr, gx = oracle.scan_bwd_softplus_f64(z, rate, want_y, go)
+    np.testing.assert_allclose(gx, xt.grad.numpy(), rtol=1e-11, atol=1e-11)
+    np.testing.assert_allclose(gz, zt.grad.numpy(), rtol=1e-11, atol=1e-11)
+    np.testing.assert_allclose(gr, rt.grad.numpy(), rtol=1e-11, atol=1e-11)
+
+
+def test_softplus_gates_limits():
+    z = np.array([[[-50.0, 0.0, 50.0]]])
+    g = oracle.softplus_gates_f64(z, np.array([2.0]))
+    np.testing.assert_allclose(g, [[[np.exp(-2 * np.log1p(np.exp(-50.0))), 0.25, np.exp(-100.0)]]],
+                               rtol=1e-12)
