@@ -232,18 +232,20 @@ def test_channel_last_validation(cl_lib):
 
 def test_channel_last_workspace_plan(cl_lib):
     """One pass when batch x strips (64 16-byte vectors each) reaches 512; otherwise segments
-    of >= 64 steps aiming at 8192 wave tasks, one (A, B) pair of 8 bytes per segment per
-    column."""
+    of about 1024 steps, more if needed for 1024 wave tasks, never below 64 steps; one
+    (A, B) pair of 8 bytes per segment per column."""
     w = cl_lib.fpscan_workspace_bytes_cl
     assert w(64, 1024, 8192, 8192, 0, 0) == 0  # 64 x 32 strips: one pass
     assert w(64, 256, 4096, 4096, 0, 0) == 0  # config 5 in channel-last form: 1024 strips
     assert w(16, 4096, 8192, 8192, 0, 0) == 0  # 512 strips
     assert w(1, 100, 64, 64, 0, 0) == 0  # too short to cut (< 2 segments of 64)
-    # bf16 (8, 65536, 1024): 8 x 2 strips -> 512 segments of 128 steps
-    assert w(8, 65536, 1024, 1024, 2, 0) == 512 * 8 * 1024 * 8
-    assert w(8, 65536, 1024, 1024, 2, 1) == 512 * 8 * 1024 * 8
-    # fp32 (4, 4096, 8192): 4 x 32 strips -> 64 segments of 64 steps
-    assert w(4, 4096, 8192, 8192, 0, 0) == 64 * 4 * 8192 * 8
+    # bf16 (8, 65536, 1024): 8 x 2 strips -> 64 segments of 1024 steps (1024 tasks)
+    assert w(8, 65536, 1024, 1024, 2, 0) == 64 * 8 * 1024 * 8
+    assert w(8, 65536, 1024, 1024, 2, 1) == 64 * 8 * 1024 * 8
+    # fp32 (4, 4096, 8192): 4 x 32 strips -> 8 segments of 512 steps (1024 tasks)
+    assert w(4, 4096, 8192, 8192, 0, 0) == 8 * 4 * 8192 * 8
+    # bf16 (4, 8192, 512): 4 strips -> 128 segments of 64 steps (capped by seqlen / 64)
+    assert w(4, 8192, 512, 512, 2, 0) == 128 * 4 * 512 * 8
     # capped by seqlen / 64 segments: fp32 (1, 1000, 64) -> 15 segments of 67 steps
     assert w(1, 1000, 64, 64, 0, 0) == 15 * 1 * 64 * 8
     assert w(1, 100, 64, 64, 0, 7) == 0  # unknown op
