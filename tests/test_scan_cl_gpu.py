@@ -274,3 +274,47 @@ def test_config4_channel_last_b8_l65536_d1024(dtype):
     gg_ref, gx_ref = oracle.scan_bwd_f64_channel_last(sel(g), sel(out), sel(go))
     check(sel(gx), gx_ref, dtype, "c4 cl grad_tokens")
     check(sel(gg), gg_ref, dtype, "c4 cl grad_gates")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("segmented", [False, True], ids=["one-pass", "segmented"])
+def test_padded_strides_through_the_c_abi(lib, dtype, segmented):
+    """(batch, seqlen, dim) views of a larger buffer: stride_t = dim + pad, stride_b = seqlen *
+    stride_t + pad2; the padding must come back untouched."""
+    B, L, D = 2, 3000, 96
+    vec = 16 // torch.empty((), dtype=dtype).element_size()
+    st = D + 4 * vec
+    sb = L * st + 2 * vec
+    g, x = cl_inputs(B, L, D, dtype, seed=4)
+    go = torch.randn(B, L, D, generator=torch.Generator().manual_seed(2)).to(dtype)
+
+    def embed(t, fill):
+        buf = torch.full((B * sb,), fill, dtype=dtype)
+        buf.as_strided((B, L, D), (sb, st, 1)).copy_(t)
+        return buf.to(DEVICE)
+
+    def view(buf):
+        return buf.as_strided((B, L, D), (sb, st, 1))
+
+    gb, xb, gob = embed(g, 7.0), embed(x, 7.0), embed(go, 7.0)
+    outb, ggb, gxb = (embed(torch.zeros_like(x), -3.0) for _ in range(3))
+    code = _CODE[dtype]
+    stream = torch.cuda.current_stream().cuda_stream
+    nb = lib.fpscan_workspace_bytes_cl(B, L, D, st, code, 0) if segmented else 0
+    ws = torch.empty(max(nb, 8), dtype=torch.uint8, device=DEVICE)
+    assert (nb > 0) == segmented
+    assert lib.fpscan_scan_fwd_cl(gb.data_ptr(), xb.data_ptr(), outb.data_ptr(), B, L, D, sb, st,
+                                  code, 0, ws.data_ptr() if nb else None, nb, stream) == 0
+    assert lib.fpscan_scan_bwd_cl(gb.data_ptr(), outb.data_ptr(), gob.data_ptr(), ggb.data_ptr(),
+                                  gxb.data_ptr(), B, L, D, sb, st, code,
+                                  ws.data_ptr() if nb else None, nb, stream) == 0
+    torch.cuda.synchronize()
+    out = view(outb).cpu()
+    check(out, oracle.scan_f64_channel_last(g, x), dtype, "cl strided fwd")
+    gg_ref, gx_ref = oracle.scan_bwd_f64_channel_last(g, out, go)
+    check(view(gxb).cpu(), gx_ref, dtype, "cl strided grad_tokens")
+    check(view(ggb).cpu(), gg_ref, dtype, "cl strided grad_gates")
+    mask = torch.ones(B * sb, dtype=torch.bool)
+    mask.as_strided((B, L, D), (sb, st, 1)).fill_(False)
+    for buf in (outb, ggb, gxb):
+        assert (buf.cpu()[mask] == -3.0).all(), "padding was written"

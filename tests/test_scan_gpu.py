@@ -503,3 +503,57 @@ def test_tiled_and_streaming_paths_agree_and_default_is_tiled_when_large():
     rows = torch.linspace(0, 8191, 16).long()
     gs, xs = g.reshape(8192, -1)[rows].cpu(), x.reshape(8192, -1)[rows].cpu()
     check(tiled.reshape(8192, -1)[rows], oracle.scan_f64(gs, xs), torch.bfloat16, "tiled c4")
+
+
+# ------------------------------------------------------------------ padded strides (C ABI)
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("L", [64, 4096, 65536])
+@pytest.mark.parametrize("tiled", [False, True], ids=["stream", "tiled"])
+def test_padded_strides_through_the_c_abi(dtype, L, tiled):
+    """Rows of a larger buffer: stride_d = L + pad, stride_b = dim * stride_d + pad2. Only
+    the (batch, dim, seqlen) view may change; the padding must come back untouched."""
+    lib = _abi()
+    B, D = 2, 3
+    vec = 16 // torch.empty((), dtype=dtype).element_size()
+    sd = L + 8 * vec
+    sb = D * sd + 4 * vec
+    g, x = make_inputs(B, D, L, dtype, seed=L + tiled)
+    go = torch.randn(B, D, L, generator=torch.Generator().manual_seed(1)).to(dtype)
+
+    def embed(t, fill):
+        buf = torch.full((B * sb,), fill, dtype=dtype)
+        view = buf.as_strided((B, D, L), (sb, sd, 1))
+        view.copy_(t)
+        return buf.to(DEVICE)
+
+    def view(buf):
+        return buf.as_strided((B, D, L), (sb, sd, 1))
+
+    gb, xb, gob = embed(g, 7.0), embed(x, 7.0), embed(go, 7.0)
+    outb, ggb, gxb = embed(torch.zeros_like(x), -3.0), embed(torch.zeros_like(x), -3.0), \
+        embed(torch.zeros_like(x), -3.0)
+    lib.fpscan_set_tiling(2 if tiled else 1)
+    try:
+        stream = torch.cuda.current_stream().cuda_stream
+        code = _CODE[dtype]
+        nb = lib.fpscan_workspace_bytes(B, D, L, code, 0) if tiled else 0
+        ws = torch.empty(max(nb, 8), dtype=torch.uint8, device=DEVICE)
+        assert lib.fpscan_scan_fwd(gb.data_ptr(), xb.data_ptr(), outb.data_ptr(), B, D, L, sb, sd,
+                                   code, 0, ws.data_ptr() if nb else None, nb, stream) == 0
+        nb = lib.fpscan_workspace_bytes(B, D, L, code, 1) if tiled else 0
+        ws = torch.empty(max(nb, 8), dtype=torch.uint8, device=DEVICE)
+        assert lib.fpscan_scan_bwd(gb.data_ptr(), outb.data_ptr(), gob.data_ptr(), ggb.data_ptr(),
+                                   gxb.data_ptr(), B, D, L, sb, sd, code,
+                                   ws.data_ptr() if nb else None, nb, stream) == 0
+        torch.cuda.synchronize()
+    finally:
+        lib.fpscan_set_tiling(0)
+    out = view(outb).cpu()
+    check(out, oracle.scan_f64(g, x), dtype, f"strided fwd L{L}")
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g, out, go)
+    check(view(gxb).cpu(), gx_ref, dtype, f"strided grad_tokens L{L}")
+    check(view(ggb).cpu(), gg_ref, dtype, f"strided grad_gates L{L}")
+    mask = torch.ones(B * sb, dtype=torch.bool)
+    mask.as_strided((B, D, L), (sb, sd, 1)).fill_(False)
+    for buf in (outb, ggb, gxb):
+        assert (buf.cpu()[mask] == -3.0).all(), "padding was written"
