@@ -458,100 +458,13 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
 // Workspace layout (8-byte words): [0, ntiles) tile status, [ntiles] wait overruns,
 // [ntiles + kCounterStride * (1 + g)] claim counter of group g.
 // ---------------------------------------------------------------------------------------
-constexpr uint64_t kNotPublished = ~0ull;
-constexpr int kSpinLimit = 1 << 16;  // polls of ~1 us each (a device-coherent load)
 
-__device__ __forceinline__ uint32_t canonical_bits(float v) {
-  return v != v ? 0x7fc00000u : __float_as_uint(v);
-}
-
-__device__ __forceinline__ uint64_t pack_map(float A, float B) {
-  return ((uint64_t)canonical_bits(B) << 32) | canonical_bits(A);
-}
-
-constexpr int kClaimGroups = 8;
-constexpr int kCounterStride = 16;  // words: each counter on its own 128-byte line
-constexpr int kStatusExtraWords = kCounterStride * (1 + kClaimGroups);
-
-__global__ void __launch_bounds__(256) clear_status(uint64_t* __restrict__ status, int64_t ntiles) {
-  const int64_t n = ntiles + kStatusExtraWords;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-    status[i] = (i < ntiles) ? kNotPublished : 0ull;
-}
-
-// Tile claims, made by one lane per workgroup. One counter at one address serialises at the
-// memory side (measured: about 70 claims per microsecond, fewer than a bf16 forward scan
-// finishes tiles), so the rows are split into kClaimGroups contiguous ranges with a counter
-// each. A workgroup starts in group blockIdx % kClaimGroups (its XCD under round-robin
-// dispatch) and, when that one is used up, moves to the group with the most tiles left. A
-// row never spans two groups and tiles of a group are claimed in order, so a tile's
-// predecessors are always claimed before it. Claims are issued two steps before their tile
-// is needed (an atomic at the memory side takes a few microseconds under full streaming
-// load), so each claim is kept with the group it was made in. In the main loop every lane of every wave issues the claim as a
-// buffer atomic that is out of range except in the leader's lane: a claim inside a branch, or
-// any use of its result before it is resolved, makes the compiler wait for it together with
-// every load issued before it. Counters are the low 32 bits of their words.
-struct Claim {
-  uint32_t raw;
-  int grp;
-};
-
-struct Claims {
-  uint32_t counters_off;  // byte offset of group 0's counter in the status buffer
-  const uint32_t* counters;
+// Claim groups of the row kernel: group g holds rows [g rows / 8, (g + 1) rows / 8), each of
+// 2^tpr_log2 tiles.
+struct RowGroups {
   int64_t rows;
   int tpr_log2;
-  int grp;
-
-  __device__ int64_t group_first(int g) const {
-    return ((int64_t)g * rows / kClaimGroups) << tpr_log2;
-  }
-  __device__ uint32_t counter_off() const {
-    return counters_off + (uint32_t)(grp * kCounterStride * sizeof(uint64_t));
-  }
-  // Straight-line claim: `mine` selects the one lane that really claims.
-  __device__ Claim issue(Rsrc st, bool mine) const {
-    return Claim{(uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
-                     1, st, mine ? counter_off() : kNoOffset, 0, 0),
-                 grp};
-  }
-  // The group with the most unclaimed tiles, or -1 when every tile is claimed. All counters
-  // are read at once (one round trip).
-  __device__ int pick_group() const {
-    uint32_t c[kClaimGroups];
-#pragma unroll
-    for (int g = 0; g < kClaimGroups; ++g)
-      c[g] = __hip_atomic_load(counters + 2 * kCounterStride * g, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    int best = -1;
-    int64_t best_left = 0;
-#pragma unroll
-    for (int g = 0; g < kClaimGroups; ++g) {
-      const int64_t left = group_first(g + 1) - group_first(g) - (int64_t)c[g];
-      if (left > best_left) {
-        best_left = left;
-        best = g;
-      }
-    }
-    return best;
-  }
-  // The tile a claim stands for: a tile index, `bubble` when its group was used up (claims
-  // then go to the group with the most tiles left), or `done` once every tile is claimed.
-  __device__ int64_t resolve(Claim c, int64_t bubble, int64_t done) {
-    const int64_t lo = group_first(c.grp);
-    if (lo + (int64_t)c.raw < group_first(c.grp + 1)) return lo + (int64_t)c.raw;
-    if (c.grp != grp) return bubble;  // made before the move to the current group
-    const int g = pick_group();
-    if (g < 0) return done;
-    grp = g;
-    return bubble;
-  }
-  // Claims until a tile or `done` comes back (start-up, leader only: waits for each atomic).
-  __device__ int64_t next_now(Rsrc st, int64_t bubble, int64_t done) {
-    int64_t t = bubble;
-    while (t == bubble) t = resolve(issue(st, true), bubble, done);
-    return t;
-  }
+  __device__ int64_t first(int g) const { return ((int64_t)g * rows / kClaimGroups) << tpr_log2; }
 };
 
 // Per-slot state of the tile ring: the tile, its row resources, its segment in the row and
@@ -563,27 +476,6 @@ struct TileSlot {
   int64_t tile;
   int seg;
 };
-
-// Status words go through a buffer resource too: every lane and wave issues the same
-// instructions, and the ones that must not touch memory use kNoOffset (reads return 0, writes
-// are dropped). Straight-line code keeps the compiler's wait counts partial, which is what
-// keeps the operand ring in flight. The cache policy is the device-coherent one (sc1), the
-// same instruction an agent-scope relaxed atomic load/store of 64 bits compiles to here.
-constexpr int kCacheCoherent = 16;
-
-__device__ __forceinline__ uint64_t status_load(Rsrc r, uint32_t off) {
-  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-  const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCacheCoherent));
-  return ((uint64_t)v.y << 32) | v.x;
-}
-
-__device__ __forceinline__ void status_store(Rsrc r, uint32_t off, uint64_t word) {
-  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-  u32x2 v;
-  v.x = (uint32_t)word;
-  v.y = (uint32_t)(word >> 32);
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kCacheCoherent);
-}
 
 template <class E, int kMode, int TW>
 __device__ __forceinline__ void tile_setup(const Args& a, TileSlot<kMode>& ts, int64_t tile,
@@ -657,9 +549,9 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
 
   // Claim results: a tile index, kBubble (no tile this step, more to come) or kDone.
   const int64_t kBubble = ntiles, kDone = ntiles + 1;
-  Claims claims{(uint32_t)((ntiles + kCounterStride) * sizeof(uint64_t)),
-                reinterpret_cast<const uint32_t*>(status + ntiles + kCounterStride),
-                ntiles >> tpr_log2, tpr_log2, (int)(blockIdx.x % kClaimGroups)};
+  Claims<RowGroups> claims{(uint32_t)((ntiles + kCounterStride) * sizeof(uint64_t)),
+                           reinterpret_cast<const uint32_t*>(status + ntiles + kCounterStride),
+                           RowGroups{ntiles >> tpr_log2, tpr_log2}, (int)(blockIdx.x % kClaimGroups)};
   // leader: claims in flight. Step u of the unrolled ring issues into pending[u] and resolves
   // pending[(u + D) % N], issued two steps earlier; no copies, which would wait for the atomic.
   Claim pending[N];
@@ -1111,6 +1003,11 @@ int validate(int64_t batch, int64_t dim, int64_t seqlen, int64_t stride_b, int64
 }
 
 }  // namespace
+
+// Path selection set by fpscan_set_tiling, read by the channel-last launcher as well.
+namespace fpscan_detail {
+int tiling_mode() { return g_tiling.load(std::memory_order_relaxed); }
+}  // namespace fpscan_detail
 
 extern "C" {
 

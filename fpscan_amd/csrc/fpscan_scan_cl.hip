@@ -23,8 +23,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "fpscan_hip.h"
 #include "scan_common.h"
+
+
+namespace fpscan_detail {
+int tiling_mode();  // fpscan_set_tiling's setting (fpscan_scan.hip)
+}  // namespace fpscan_detail
 
 namespace {
 
@@ -52,6 +59,8 @@ struct ClArgs {
   int32_t seg_len;   // time steps per segment
   int32_t nseg;
   int32_t strips;    // per batch: ceil(dim / (64 V))
+  int64_t chains;    // tiled path: batch * strips64
+  int64_t strips64;  // tiled path, per batch: ceil(dim / 64)
 };
 
 // Loaded operands of one time step for one lane.
@@ -231,6 +240,439 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 }
 
 // ---------------------------------------------------------------------------------------
+// Tiled channel-last scan: one pass (3 N s bytes forward) with a decoupled look-back along
+// the time axis, for problems with too few strips to fill the device one wave per strip.
+//
+// A chain is one batch's 64 consecutive columns over the whole time axis; a tile is
+// 16 R consecutive time steps of one chain (R = V: 128 steps for 2-byte types, 64 for fp32),
+// one workgroup of 16 waves. Lane r + R c of wave w holds the 16-byte vector c (V columns) of
+// time step w R + r of the tile, so every wave instruction reads R rows x 128 or 256
+// contiguous bytes. Per tile:
+//   1. each lane turns its step into V affine maps (A, B) = (gate, token);
+//   2. a DPP scan over the R row groups of the wave (R consecutive lanes per column vector)
+//      gives each lane the inclusive map of rows 0..r of its wave, and the last row group
+//      the wave's total;
+//   3. wave totals go through LDS; wave w scans the 16 wave totals of columns 4w..4w+3 with
+//      one 16-lane DPP row each, which yields the prefix entering every wave and the tile's
+//      aggregate map per column, published at once (one 64-bit word per column);
+//   4. the carry into the tile, per column, from its predecessors (below); each lane then
+//      has y = M(carry) for its V columns, with M its composed map, and stores;
+//   5. wave 0 publishes the tile's last value per column (a 32-bit word), y_end = A c + B.
+// Look-back: the predecessors of tile k are the earlier tiles of its chain, k-1, k-2, ...
+// The carry into k is always composed the same way, so results do not depend on timing:
+//     carry(k) = agg(k-1) o agg(k-2) o agg(k-3) applied to y_end(k-4)
+// (fewer maps and the zero state near the chain start). Tiles are claimed in order (Claims
+// over chain groups: within a group all chains' tile 0, then all chains' tile 1, ...), so a
+// tile's predecessors were claimed before it. An aggregate is published by a reduce, which
+// never waits; y_end(k-4) by a finish, which waits only for earlier tiles. So the workgroup
+// holding the lowest unfinished tile of a group always progresses (the row kernel's argument,
+// by induction over tile order). As in the row kernel, the words a finish needs are loaded
+// one step ahead (here right after the tile's reduce, kClDefer = 1) and only missing ones are
+// polled (bounded, device-coherent). With about 4 * kClBlocksPerChain tiles of a chain in
+// flight, tile k-4 has usually finished by then.
+//
+// Workspace: ntiles * 64 aggregate words (8 bytes; tile-major, one per column), ntiles * 64
+// end values (4 bytes), then the overrun word and claim counters as in the row kernel.
+// All-ones marks an unpublished word (NaNs are canonicalised, so data never has that form).
+// ---------------------------------------------------------------------------------------
+constexpr int kClTileWaves = 16;
+constexpr int kClTileCols = 64;  // columns per chain and tile
+constexpr int kClDefer = 1;      // steps between a tile's reduce and its finish
+constexpr int kClAggs = 3;       // aggregates composed onto a predecessor's end value
+static_assert(kClTileWaves * 4 == kClTileCols, "wave w scans the totals of columns 4w..4w+3");
+
+constexpr uint32_t kEndNotPublished = ~0u;
+
+__device__ __forceinline__ uint32_t end_load(Rsrc r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCacheCoherent);
+}
+
+__device__ __forceinline__ void end_store(Rsrc r, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kCacheCoherent);
+}
+
+// Whether one of the first n predecessor aggregates is still unpublished.
+template <int K>
+__device__ __forceinline__ bool agg_missing(const uint64_t (&words)[K], int n) {
+  bool missing = false;
+#pragma unroll
+  for (int j = 0; j < K; ++j) missing = missing || (j < n && words[j] == kNotPublished);
+  return missing;
+}
+
+// Claim groups of chains: group g holds chains [g chains / 8, (g + 1) chains / 8), each of
+// nseg tiles, claimed segment-major.
+struct ChainGroups {
+  int64_t chains;
+  int64_t nseg;
+  __device__ int64_t chain_lo(int g) const {
+    return (int64_t)(((uint64_t)g * (uint64_t)chains) / kClaimGroups);
+  }
+  __device__ int64_t first(int g) const { return chain_lo(g) * nseg; }
+};
+
+// Time steps per tile: 16 waves of R = V row groups (one 16-byte vector of V columns per lane).
+template <class E>
+constexpr int cl_tile_steps() {
+  return kClTileWaves * E::V;
+}
+
+template <int kMode>
+struct ClTile {
+  u32x4 v[kMode == kBwd ? 3 : 2];  // this lane's operands (bwd: gates t+1, grad_out t, out t-1)
+  int64_t base;    // element offset of the first row of the tile's buffer range, all tensors
+  int32_t bytes;   // buffer range: the tile's rows plus one on each side
+  uint32_t off;    // byte offset of this lane's vector in the range; kNoOffset: none
+  bool first;      // this lane holds the chain's first step (processing order)
+  int64_t tile;    // ntiles: no tile
+  int seg;         // position of the tile along its chain (processing order)
+  int nch;         // chains of the tile's claim group: the distance to its predecessor
+};
+
+__device__ __forceinline__ Rsrc cl_tile_rsrc(const void* p, int64_t base, int size, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(static_cast<const char*>(p)) + base * size, (short)0, bytes, kRsrcWord3);
+}
+
+// Locates tile `tile` of claim group `g` and issues its operand loads (lanes without an
+// element load nothing).
+template <class E, int kMode>
+__device__ __forceinline__ void cl_tile_setup(const ClArgs& a, ClTile<kMode>& ts, int64_t tile,
+                                              int g, int64_t ntiles, const ChainGroups& cg,
+                                              int w, int c, int r) {
+  constexpr int V = E::V;
+  constexpr int T = cl_tile_steps<E>();
+  constexpr bool kReverse = kMode != kFwd;
+  const int L = a.seqlen;
+  ts.tile = tile;
+  const bool live = tile < ntiles;
+  const int64_t c_lo = cg.chain_lo(g);
+  const int nch = live ? (int)(cg.chain_lo(g + 1) - c_lo) : 1;
+  const uint32_t k = live ? (uint32_t)(tile - c_lo * cg.nseg) : 0u;
+  // integer division runs on the vector unit: move the (uniform) results back to scalars
+  const int seg = __builtin_amdgcn_readfirstlane((int)(k / (uint32_t)nch));
+  const int64_t chain = c_lo + (int64_t)(k - (uint32_t)seg * (uint32_t)nch);
+  const int64_t b = __builtin_amdgcn_readfirstlane((uint32_t)chain / (uint32_t)a.strips64);
+  const int strip = (int)(chain - b * a.strips64);
+  ts.seg = seg;
+  ts.nch = nch;
+  // processing positions [p0, p1) of the tile; time rows [lo, hi)
+  const int p0 = seg * T;
+  const int p1 = min(p0 + T, L);
+  const int lo = kReverse ? L - p1 : p0;
+  const int hi = kReverse ? L - p0 : p1;
+  const int r0 = lo > 0 ? lo - 1 : 0;
+  const int r1 = hi < L ? hi + 1 : L;
+  const uint32_t row_bytes = (uint32_t)(a.stride_t * E::kSize);
+  ts.base = live ? b * a.stride_b + (int64_t)r0 * a.stride_t : 0;
+  ts.bytes = live ? (int32_t)((uint32_t)(r1 - r0) * row_bytes) : 0;
+  const int p = p0 + w * V + r;
+  const int col = strip * kClTileCols + c * V;
+  const bool mine = live && p < p1 && col < a.dim;
+  const int t = kReverse ? L - 1 - p : p;
+  ts.first = p == 0;
+  ts.off = mine ? (uint32_t)(t - r0) * row_bytes + (uint32_t)col * E::kSize : kNoOffset;
+  const Rsrc in0 = cl_tile_rsrc(a.in0, ts.base, E::kSize, ts.bytes);
+  const Rsrc in1 = cl_tile_rsrc(a.in1, ts.base, E::kSize, ts.bytes);
+  if constexpr (kMode == kBwd) {
+    const Rsrc in2 = cl_tile_rsrc(a.in2, ts.base, E::kSize, ts.bytes);
+    ts.v[0] = bld16(in0, mine && t + 1 < L ? ts.off + row_bytes : kNoOffset);
+    ts.v[1] = bld16(in1, ts.off);
+    ts.v[2] = bld16(in2, mine && t >= 1 ? ts.off - row_bytes : kNoOffset);
+  } else {
+    ts.v[0] = bld16(in0, ts.off);
+    ts.v[1] = bld16(in1, ts.off);
+  }
+}
+
+template <class E, int kMode, int D>
+__global__ void __launch_bounds__(64 * kClTileWaves)
+scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntiles) {
+  constexpr int V = E::V;
+  constexpr int R = V;  // row groups per wave
+  constexpr int N = D + 2;
+  constexpr int kPad = 2;             // LDS row padding (f32x2), keeps 16-byte alignment
+  static_assert(N % D == 0, "the unrolled ring must map each step to a fixed deferral slot");
+  static_assert(R * (kClTileCols / V) == 64, "a wave is R row groups of 64 columns");
+
+  __shared__ f32x2 exch[kClTileWaves][kClTileCols + kPad];  // wave totals
+  __shared__ f32x2 pref[kClTileWaves][kClTileCols + kPad];  // prefix entering each wave
+  __shared__ f32x2 aggs[D][kClTileCols];                    // tile aggregates, by deferral slot
+  __shared__ float carry_in[kClTileCols];
+  __shared__ int64_t claimed;
+  __shared__ int claimed_grp;
+  __shared__ int64_t first_tiles[2];
+  __shared__ int first_grps[2];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane % R;  // row group: consecutive lanes, so that the scan is a DPP one
+  const int c = lane / R;  // column group: columns V c .. V c + V - 1
+  const bool leader = threadIdx.x == 0;
+  const int L = a.seqlen;
+  // aggregate words, then end values (32-bit) from word nagg on, then the extra words
+  const int64_t nagg = ntiles * kClTileCols;
+  const int64_t nstatus = nagg + nagg / 2;
+  const uint32_t ends_off = (uint32_t)(nagg * sizeof(uint64_t));
+  const Rsrc st = __builtin_amdgcn_make_buffer_rsrc(
+      status, (short)0, (int)((nstatus + kStatusExtraWords) * sizeof(uint64_t)), kRsrcWord3);
+  const ChainGroups cg{a.chains, a.nseg};
+
+  const int64_t kBubble = ntiles, kDone = ntiles + 1;
+  Claims<ChainGroups> claims{(uint32_t)((nstatus + kCounterStride) * sizeof(uint64_t)),
+                             reinterpret_cast<const uint32_t*>(status + nstatus + kCounterStride),
+                             cg, (int)(blockIdx.x % kClaimGroups)};
+  Claim pending[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) pending[i] = Claim{0, 0};
+  bool claims_done = false;
+  if (leader) {
+    // a tile that next_now returns comes from the current group
+    const int64_t t0 = claims.next_now(st, kBubble, kDone);
+    first_grps[0] = claims.grp;
+    const int64_t t1 = (t0 == kDone) ? kDone : claims.next_now(st, kBubble, kDone);
+    first_grps[1] = claims.grp;
+    first_tiles[0] = t0;
+    first_tiles[1] = t1;
+    claims_done = t1 == kDone;
+  }
+  __syncthreads();
+  // The two steps before the loop issue what a steady-state step issues, in the same order
+  // (predecessor words, here out of range; the claim two steps ahead; the refill), so that
+  // the compiler's wait counts at the loop head are the steady-state ones. Otherwise the
+  // path into the loop makes it wait there for the words and the claim just issued.
+  uint64_t held_agg[kClAggs];
+  uint32_t held_end;
+  ClTile<kMode> ring[N];
+#pragma unroll
+  for (int i = 2; i < N; ++i) {  // filled at the end of the first steps
+    ring[i].tile = ntiles;
+    ring[i].seg = 0;
+    ring[i].nch = 1;
+    ring[i].base = 0;
+    ring[i].bytes = 0;
+    ring[i].off = kNoOffset;
+    ring[i].first = false;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < kClAggs; ++j) held_agg[j] = status_load(st, kNoOffset);
+    held_end = end_load(st, kNoOffset);
+    pending[N - 2 + i] = claims.issue(st, leader && !claims_done);
+    cl_tile_setup<E, kMode>(a, ring[i],
+                            min(__builtin_amdgcn_readfirstlane(first_tiles[i]), ntiles),
+                            __builtin_amdgcn_readfirstlane(first_grps[i]), ntiles, cg, w, c, r);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // per deferral slot: the map from the tile's carry to this lane's value, per column (the
+  // prefix entering its wave, then its wave's row groups up to its own)
+  float held_A[D][V], held_B[D][V];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      held_A[i][e] = 1.0f;
+      held_B[i][e] = 0.0f;
+    }
+  }
+  bool all_claimed = false;
+
+  for (;;) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      ClTile<kMode>& cur = ring[u];
+      ClTile<kMode>& fin = ring[(u + 2) % N];
+      const int hs = u % D;
+      const bool cur_live = cur.tile < ntiles;
+      const bool fin_live = fin.tile < ntiles;
+
+      // (1) the current tile: this lane's maps (gate, token) per column, then an inclusive
+      // scan over the R row groups of the wave (lanes R c .. R c + R - 1, one DPP segment);
+      // the last row group ends with the wave's total
+      float pa[V], pb[V];
+      {
+        float g[V];
+        E::unpack(cur.v[0], g);
+        E::unpack(cur.v[1], pb);
+        // the chain's first step keeps gate 1: forward and reverse never use its gate, and the
+        // backward's shifted gate is gates[L] = 1; lanes without an element are the identity
+        const bool none = cur.off == kNoOffset;
+        const bool unit = none || cur.first;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          pa[e] = unit ? 1.0f : g[e];
+          pb[e] = none ? 0.0f : pb[e];
+          segment_scan<R>(pa[e], pb[e], r);
+          if (r == R - 1) exch[w][c * V + e] = f32x2{pa[e], pb[e]};
+        }
+      }
+
+      // (2) the finishing tile's carry per column from its predecessors' words (wave 0; the
+      // other waves hold out-of-range words, zeros, and compute a carry nobody uses)
+      {
+        const int na = min(fin.seg, kClAggs);  // aggregates composed (uniform)
+        if (__builtin_amdgcn_ballot_w64(agg_missing(held_agg, na) ||
+                                        (fin.seg > kClAggs && held_end == kEndNotPublished)) != 0) {
+          // a predecessor has not published yet: poll the missing words (bounded; once any
+          // wait of this launch has overrun, which a correct launch never does, the others
+          // give up at once, so that the launch still ends soon)
+          const bool overran = __hip_atomic_load(status + nstatus, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT) != 0;
+          for (int it = overran ? kSpinLimit : 0;; ++it) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int j = 0; j < kClAggs; ++j) {
+              if (j < na && held_agg[j] == kNotPublished)
+                held_agg[j] = __hip_atomic_load(
+                    status + (fin.tile - (int64_t)(j + 1) * fin.nch) * kClTileCols + lane,
+                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (fin.seg > kClAggs && held_end == kEndNotPublished)
+              held_end = __hip_atomic_load(
+                  reinterpret_cast<const uint32_t*>(status + nagg) +
+                      (fin.tile - (int64_t)(kClAggs + 1) * fin.nch) * kClTileCols + lane,
+                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (__builtin_amdgcn_ballot_w64(agg_missing(held_agg, na) ||
+                                            (fin.seg > kClAggs && held_end == kEndNotPublished)) == 0)
+              break;
+            if (it == kSpinLimit) {
+              if (lane == 0)
+                __hip_atomic_fetch_add(status + nstatus, 1ull, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+              break;  // only after an overrun: the words still missing count as zeros
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < kClAggs; ++j)
+            held_agg[j] = held_agg[j] == kNotPublished ? 0ull : held_agg[j];
+          held_end = held_end == kEndNotPublished ? 0u : held_end;
+        }
+        // carry = agg(k-1) o ... o agg(k-na) applied to y_end(k-na-1), or to the zero state
+        float carry = fin.seg > kClAggs ? __uint_as_float(held_end) : 0.0f;
+#pragma unroll
+        for (int j = kClAggs - 1; j >= 0; --j) {
+          if (j < na) {
+            const uint64_t word = held_agg[j];
+            carry = fmaf(__uint_as_float((uint32_t)word), carry,
+                         __uint_as_float((uint32_t)(word >> 32)));
+          }
+        }
+        // wave 0 hands the carries on and publishes the finishing tile's end values, which
+        // tile k+4 reads (the store is issued by every wave, out of range elsewhere: a store
+        // inside a branch would leave the compiler unsure how many memory operations follow
+        // each load)
+        if (w == 0) carry_in[lane] = carry;
+        const f32x2 agg = aggs[hs][lane];
+        const bool publish = w == 0 && fin_live && fin.seg + kClAggs + 1 < a.nseg;
+        end_store(st,
+                  publish ? ends_off + (uint32_t)((fin.tile * kClTileCols + lane) * sizeof(uint32_t))
+                          : kNoOffset,
+                  canonical_bits(fmaf(agg.x, carry, agg.y)));
+      }
+      if (leader) {
+        const int64_t t = claims_done ? kDone : claims.resolve(pending[(u + D) % N], kBubble, kDone);
+        claims_done = t == kDone;
+        claimed = t;
+        claimed_grp = pending[(u + D) % N].grp;  // the group of a tile that resolve returns
+      }
+      lds_barrier();
+      const int64_t claim = __builtin_amdgcn_readfirstlane(claimed);
+      const int claim_grp = __builtin_amdgcn_readfirstlane(claimed_grp);
+      all_claimed = claim == kDone;
+
+      // (3) the current tile's wave prefixes and aggregate (wave w: columns 4w..4w+3)
+      {
+        const int i = lane & 15;
+        const int col = 4 * w + (lane >> 4);
+        const f32x2 e = exch[i][col];
+        float eA = e.x, eB = e.y;
+        combine_from<kRowShr1>(eA, eB);
+        combine_from<kRowShr2>(eA, eB);
+        combine_from<kRowShr4>(eA, eB);
+        combine_from<kRowShr8>(eA, eB);
+        if (i < 15) pref[i + 1][col] = f32x2{eA, eB};
+        if (i == 15) aggs[hs][col] = f32x2{eA, eB};
+        const bool publish = cur_live && i == 15;
+        status_store(st,
+                     publish ? (uint32_t)((cur.tile * kClTileCols + col) * sizeof(uint64_t))
+                             : kNoOffset,
+                     pack_map(eA, eB));
+      }
+
+      // (4) finish the oldest deferred tile
+      {
+        float y[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) y[e] = fmaf(held_A[hs][e], carry_in[c * V + e], held_B[hs][e]);
+        const Rsrc out0 = cl_tile_rsrc(a.out0, fin.base, E::kSize, fin.bytes);
+        bst16(out0, fin.off, E::pack(y));
+        if constexpr (kMode == kBwd) {
+          float ys[V], o1[V];
+          E::unpack(fin.v[2], ys);
+#pragma unroll
+          for (int e = 0; e < V; ++e) o1[e] = y[e] * ys[e];
+          const Rsrc out1 = cl_tile_rsrc(a.out1, fin.base, E::kSize, fin.bytes);
+          bst16(out1, fin.off, E::pack(o1));
+        }
+      }
+      lds_barrier();
+
+      // (5) the current tile's composed maps, held until its finish
+      {
+        float PA[V], PB[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          PA[e] = 1.0f;
+          PB[e] = 0.0f;
+        }
+        if (w > 0) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const f32x2 q = pref[w][c * V + e];
+            PA[e] = q.x;
+            PB[e] = q.y;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          held_B[hs][e] = fmaf(pa[e], PB[e], pb[e]);
+          held_A[hs][e] = pa[e] * PA[e];
+        }
+      }
+
+      // (6) wave 0: the predecessor words of the tile finished next step (the current one),
+      // loaded before the refill below (vector loads return in issue order)
+      {
+        const ClTile<kMode>& nxt = ring[(u + 3) % N];
+        const bool mine = w == 0 && nxt.tile < ntiles;
+#pragma unroll
+        for (int j = 0; j < kClAggs; ++j) {
+          const int64_t p = nxt.tile - (int64_t)(j + 1) * nxt.nch;
+          held_agg[j] = status_load(
+              st, mine && j < nxt.seg ? (uint32_t)((p * kClTileCols + lane) * sizeof(uint64_t))
+                                      : kNoOffset);
+        }
+        const int64_t q = nxt.tile - (int64_t)(kClAggs + 1) * nxt.nch;
+        held_end = end_load(st, mine && nxt.seg > kClAggs
+                                    ? ends_off + (uint32_t)((q * kClTileCols + lane) * sizeof(uint32_t))
+                                    : kNoOffset);
+      }
+      pending[u] = claims.issue(st, leader && !claims_done);
+      // (7) refill the finished slot with the tile claimed two steps ago
+      cl_tile_setup<E, kMode>(a, fin, claim < ntiles ? claim : ntiles, claim_grp, ntiles, cg, w,
+                              c, r);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    bool busy = !all_claimed;
+#pragma unroll
+    for (int i = 0; i < N; ++i) busy = busy || ring[i].tile < ntiles;
+    if (!busy) break;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------
 constexpr int kClWaves = 4;  // independent waves per block
@@ -299,8 +741,108 @@ int launch_cl(const ClArgs& a, hipStream_t stream) {
   return err == hipSuccess ? FPSCAN_OK : FPSCAN_ERR_LAUNCH;
 }
 
+// Tiled path. It replaces the segments wherever one pass per strip lacks waves and there are
+// enough chains: the persistent grid is capped at kClBlocksPerChain workgroups per chain, so
+// that about 3 * kClBlocksPerChain tiles of a chain are in flight at once and the end value a
+// finishing tile needs (kClAggs + 1 tiles back) is usually published already.
+constexpr int64_t kClTileMinChains = 64;
+constexpr int64_t kClBlocksPerChain = 2;
+
+struct ClTilePlan {
+  bool use;
+  int64_t chains;
+  int64_t strips64;
+  int64_t nseg;
+  int64_t ntiles;
+  size_t bytes;  // workspace: 64 aggregates and 64 end values per tile, the overrun word and
+                 // claim counters
+};
+
+// 8-byte words of per-tile status: a 64-bit aggregate and a 32-bit end value per column.
+int64_t cl_status_words(int64_t ntiles) { return ntiles * kClTileCols * 3 / 2; }
+
+ClTilePlan plan_cl_tiles(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_t, int size,
+                         int tiling) {
+  ClTilePlan t{false, 0, 0, 0, 0, 0};
+  if (tiling == 1 || batch <= 0 || seqlen <= 0 || dim <= 0) return t;
+  const int64_t steps = size == 4 ? cl_tile_steps<F32>() : cl_tile_steps<BF16>();
+  t.strips64 = (dim + kClTileCols - 1) / kClTileCols;
+  t.chains = batch * t.strips64;
+  t.nseg = (seqlen + steps - 1) / steps;
+  t.ntiles = t.chains * t.nseg;
+  const int64_t words = cl_status_words(t.ntiles) + kStatusExtraWords;
+  if (words * (int64_t)sizeof(uint64_t) > INT32_MAX) return t;
+  if ((steps + 2) * stride_t * size > INT32_MAX) return t;
+  if (tiling == 0) {
+    const int64_t strips = (dim + 64 * cl_vec(size) - 1) / (64 * cl_vec(size));
+    if (batch * strips >= kClMinTasks || t.chains < kClTileMinChains || t.nseg < 2) return t;
+  }
+  t.use = true;
+  t.bytes = (size_t)words * sizeof(uint64_t);
+  return t;
+}
+
+constexpr int kClMaxDevices = 64;
+std::atomic<int> g_cl_resident[kClMaxDevices][9];
+
+// Workgroups of `kernel` resident at once on the current device (CUs x blocks per CU), cached
+// per device and kernel; 0 if the device cannot be queried.
+int cl_resident_blocks(const void* kernel, int slot, int threads) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kClMaxDevices) {
+    const int cached = g_cl_resident[dev][slot].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+      cus <= 0 || per_cu <= 0)
+    return 0;
+  const int n = cus * per_cu;
+  if (dev < kClMaxDevices) g_cl_resident[dev][slot].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Clears the status words and counters, then the persistent grid. -1 when the occupancy query
+// fails (the caller then takes another path).
+template <class E, int kMode>
+int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t stream) {
+  const void* kernel = reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer>);
+  const int threads = 64 * kClTileWaves;
+  const int resident = cl_resident_blocks(kernel, E::kSlot * 3 + kMode, threads);
+  if (resident <= 0) return -1;
+  uint64_t* status = static_cast<uint64_t*>(workspace);
+  int64_t ntiles = plan.ntiles;
+  int64_t nstatus = cl_status_words(ntiles);
+  const int64_t nwords = nstatus + kStatusExtraWords;
+  const int64_t clear_blocks = (nwords + 255) / 256 < 2048 ? (nwords + 255) / 256 : 2048;
+  void* cargs[] = {&status, &nstatus};
+  if (hipLaunchKernel(reinterpret_cast<const void*>(&clear_status), dim3((unsigned)clear_blocks),
+                      dim3(256), cargs, 0, stream) != hipSuccess)
+    return FPSCAN_ERR_LAUNCH;
+  int64_t grid = resident;
+  if (grid > ntiles) grid = ntiles;
+  if (grid > kClBlocksPerChain * plan.chains) grid = kClBlocksPerChain * plan.chains;
+  a.chains = plan.chains;
+  a.strips64 = plan.strips64;
+  a.nseg = (int32_t)plan.nseg;
+  a.seg_len = cl_tile_steps<E>();
+  a.ws = nullptr;
+  void* kargs[] = {&a, &status, &ntiles};
+  const hipError_t err =
+      hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), kargs, 0, stream);
+  return err == hipSuccess ? FPSCAN_OK : FPSCAN_ERR_LAUNCH;
+}
+
 template <class E, int kMode>
 int run_cl(ClArgs a, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  const ClTilePlan tiles = plan_cl_tiles(a.batch, a.seqlen, a.dim, a.stride_t, E::kSize,
+                                         fpscan_detail::tiling_mode());
+  if (tiles.use && workspace != nullptr && ws_bytes >= tiles.bytes) {
+    const int st = run_cl_tiled<E, kMode>(a, tiles, workspace, stream);
+    if (st >= 0) return st;
+  }
   const ClPlan plan = plan_cl(a.batch, a.seqlen, a.dim, a.stride_t, E::kSize);
   if (plan.nseg > 1 && workspace != nullptr && ws_bytes >= plan.bytes) {
     a.nseg = plan.nseg;
@@ -421,6 +963,9 @@ size_t fpscan_workspace_bytes_cl(int64_t batch, int64_t seqlen, int64_t dim, int
   if (size == 0 || batch <= 0 || seqlen <= 0 || dim <= 0 || seqlen > INT32_MAX) return 0;
   if (stride_t < dim || stride_t * size > (INT32_MAX / 3)) return 0;
   if (op != FPSCAN_OP_FWD && op != FPSCAN_OP_BWD) return 0;
+  const ClTilePlan tiles =
+      plan_cl_tiles(batch, seqlen, dim, stride_t, size, fpscan_detail::tiling_mode());
+  if (tiles.use) return tiles.bytes;
   return plan_cl(batch, seqlen, dim, stride_t, size).bytes;
 }
 

@@ -256,6 +256,7 @@ def set_launch_override(waves_per_row: int = 0, ring_depth: int = 0) -> None:
 
 
 def set_tiling(mode: int = 0) -> None:
-    """Path selection for long rows (process-wide): 0 automatic, 1 row streaming only,
+    """Path selection (process-wide) for long rows and channel-last scans: 0 automatic,
+    1 no tiled look-back (rows streamed; channel-last one pass per strip or segments),
     2 tiled (persistent grid with look-back) whenever the shape allows."""
     _load_extension().set_tiling(int(mode))

@@ -101,11 +101,14 @@ size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dt
  * Same semantics as fpscan_scan_fwd on the transposed data (first gate ignored, zero initial
  * state, fp32 arithmetic), without the transposes. Any seqlen >= 1; dim, stride_t and
  * stride_b multiples of 16/itemsize elements; pointers 16-byte aligned; `out` may alias
- * `tokens` or `gates` exactly. With fewer than 512 strips of 64 16-byte vectors
- * (batch * dim / (64 * 16/itemsize)) the time axis is cut into segments, which needs
- * fpscan_workspace_bytes_cl() bytes of workspace; without it the call runs one pass per strip
+ * `tokens` or `gates` exactly. With at least 512 strips of 64 16-byte vectors
+ * (batch * dim / (64 * 16/itemsize)) one wave scans each strip in one pass. With fewer, the
+ * time axis is tiled and needs fpscan_workspace_bytes_cl() bytes of workspace: with at least
+ * 64 chains (batch * dim / 64) a single pass whose tiles look back along time (3 N s bytes
+ * forward, results independent of timing), otherwise segments (aggregates, carries, then
+ * the segments again: 5 N s bytes). Without the workspace the call runs one pass per strip
  * (correct, slower), except that a batch slab of more than about 2 GiB needs the workspace
- * (FPSCAN_ERR_WORKSPACE otherwise).
+ * (FPSCAN_ERR_WORKSPACE otherwise). Calls sharing a workspace must not overlap.
  * No reference counterpart: the reference supports (batch, dim, seqlen) only and tells callers
  * of this layout to transpose in and out (README.md:94-99). */
 int fpscan_scan_fwd_cl(const void* gates, const void* tokens, void* out,
@@ -126,7 +129,8 @@ int fpscan_scan_bwd_cl(const void* gates, const void* out, const void* grad_out,
                        int dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace, in bytes, for the segmented channel-last path of this problem (0: one pass). */
+/* Workspace, in bytes, for the tiled or segmented channel-last path this problem takes (0: one
+ * pass per strip); it depends on fpscan_set_tiling's setting. */
 size_t fpscan_workspace_bytes_cl(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_t,
                                  int dtype, int op);
 
@@ -188,9 +192,12 @@ int fpscan_abi_version(void);
  * reference fixes its tiles at compile time (full_scan.cu:207-233). */
 int fpscan_set_launch_override(int waves_per_row, int ring_depth);
 
-/* Path selection for tests and tuning; process-wide. 0: automatic (tiled for problems of at
- * least 512 MiB per tensor when a workspace is given), 1: row streaming only, 2: tiled
- * whenever the row has 16..1024 sub-chunks and a workspace is given. No reference counterpart. */
+/* Path selection for tests and tuning; process-wide. 0: automatic (rows: tiled for problems
+ * of at least 512 MiB per tensor; channel-last: tiled look-back with at least 64 chains when
+ * one pass per strip lacks strips), 1: no tiled look-back (rows streamed; channel-last one
+ * pass or segments), 2: tiled whenever possible (rows with 16..1024 sub-chunks; any
+ * channel-last problem whose 130-row tile fits a 2 GiB buffer range). Tiled paths need the
+ * workspace. No reference counterpart. */
 int fpscan_set_tiling(int mode);
 
 #ifdef __cplusplus
