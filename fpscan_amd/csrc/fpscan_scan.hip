@@ -565,16 +565,22 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
     first_tiles[1] = t1;
     claims_done = t1 == kDone;
   }
-  pending[N - 2] = claims.issue(st, leader && !claims_done);
-  pending[N - 1] = claims.issue(st, leader && !claims_done);
   __syncthreads();
+  // The two steps before the loop issue what a steady-state step issues, in the same order
+  // (the predecessor word, here out of range; the claim two steps ahead; the refill), so that
+  // the compiler's wait counts at the loop head are the steady-state ones. Otherwise the path
+  // into the loop makes it wait there for the word and the claim just issued.
+  uint64_t held_word = 0;
   TileSlot<kMode> ring[N];
-  tile_setup<E, kMode, TW>(a, ring[0], min(__builtin_amdgcn_readfirstlane(first_tiles[0]), ntiles),
-                           ntiles, tpr_log2, w, lane_off);
-  __builtin_amdgcn_sched_barrier(0);
-  tile_setup<E, kMode, TW>(a, ring[1], min(__builtin_amdgcn_readfirstlane(first_tiles[1]), ntiles),
-                           ntiles, tpr_log2, w, lane_off);
-  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    held_word = status_load(st, kNoOffset);
+    pending[N - 2 + i] = claims.issue(st, leader && !claims_done);
+    tile_setup<E, kMode, TW>(a, ring[i],
+                             min(__builtin_amdgcn_readfirstlane(first_tiles[i]), ntiles), ntiles,
+                             tpr_log2, w, lane_off);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int i = 2; i < N; ++i) {  // filled at the end of the first steps
     ring[i].tile = ntiles;
@@ -587,7 +593,6 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
   // finished next, loaded one step ahead
   float held_A[D], held_B[D], held_pA[D], held_pB[D];
   bool have[D];
-  uint64_t held_word = 0;
 #pragma unroll
   for (int i = 0; i < D; ++i) {
     held_A[i] = 1.0f;
