@@ -459,14 +459,6 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
 // [ntiles + kCounterStride * (1 + g)] claim counter of group g.
 // ---------------------------------------------------------------------------------------
 
-// Claim groups of the row kernel: group g holds rows [g rows / 8, (g + 1) rows / 8), each of
-// 2^tpr_log2 tiles.
-struct RowGroups {
-  int64_t rows;
-  int tpr_log2;
-  __device__ int64_t first(int g) const { return ((int64_t)g * rows / kClaimGroups) << tpr_log2; }
-};
-
 // Per-slot state of the tile ring: the tile, its row resources, its segment in the row and
 // the operands of this wave's sub-chunk.
 template <int kMode>

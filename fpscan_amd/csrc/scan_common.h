@@ -234,6 +234,14 @@ __global__ void __launch_bounds__(256) clear_status(uint64_t* __restrict__ statu
     status[i] = (i < ntiles) ? kNotPublished : 0ull;
 }
 
+// Claim groups over rows: group g holds rows [g rows / 8, (g + 1) rows / 8), each of
+// 2^tpr_log2 tiles (the row scan's tiled kernel).
+struct RowGroups {
+  int64_t rows;
+  int tpr_log2;
+  __device__ int64_t first(int g) const { return ((int64_t)g * rows / kClaimGroups) << tpr_log2; }
+};
+
 // Tile claims, made by one lane per workgroup. One counter at one address serialises at the
 // memory side (measured: about 70 claims per microsecond, fewer than a bf16 forward scan
 // finishes tiles), so the tiles are split into kClaimGroups contiguous ranges with a counter
