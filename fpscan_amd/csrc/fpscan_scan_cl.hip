@@ -14,10 +14,11 @@
 //   Each lane carries the V independent recurrences of its vector down the time axis, so
 //   there is no cross-lane scan at all: per step, y = fma(a, y, b) on V values. One wave owns
 //   one strip of one batch over a segment of time steps, with a ring of U steps in flight.
-//   When batch x strips alone cannot fill the device, the time axis is cut into segments and
-//   three launches run: per-segment per-column aggregates (A, B) into the workspace, a carry
-//   pass over the segments of each column, then the segments again with their carry-in.
-//   That moves 5 N s bytes for the forward scan instead of 3 N s, still without transposes.
+//   When batch x strips alone cannot fill the device, the time axis is tiled instead: with
+//   enough 64-column chains, one pass over tiles of 64 columns with a look-back along time
+//   (scan_cl_tiles below, 3 N s bytes forward); otherwise segments in three launches (per-
+//   segment per-column aggregates (A, B) into the workspace, a carry pass over the segments of
+//   each column, then the segments again with their carry-in: 5 N s bytes forward).
 // All arithmetic is fp32; half types are widened exactly on load and rounded to nearest even
 // once on store.
 #include <hip/hip_runtime.h>
