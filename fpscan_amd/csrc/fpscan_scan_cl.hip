@@ -494,19 +494,21 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
       // the last row group ends with the wave's total
       float pa[V], pb[V];
       {
-        float g[V];
-        E::unpack(cur.v[0], g);
+        E::unpack(cur.v[0], pa);
         E::unpack(cur.v[1], pb);
         // the chain's first step keeps gate 1: forward and reverse never use its gate, and the
-        // backward's shifted gate is gates[L] = 1; lanes without an element are the identity
-        const bool none = cur.off == kNoOffset;
-        const bool unit = none || cur.first;
+        // backward's shifted gate is gates[L] = 1. Lanes without an element loaded zeros, the
+        // map (0, 0): such lanes are columns past dim or steps past the chain's end, and
+        // columns never mix, so it reaches no stored value.
+        if (cur.first) {
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          pa[e] = unit ? 1.0f : g[e];
-          pb[e] = none ? 0.0f : pb[e];
-          segment_scan<R>(pa[e], pb[e], r);
-          if (r == R - 1) exch[w][c * V + e] = f32x2{pa[e], pb[e]};
+          for (int e = 0; e < V; ++e) pa[e] = 1.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) segment_scan<R>(pa[e], pb[e], r);
+        if (r == R - 1) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) exch[w][c * V + e] = f32x2{pa[e], pb[e]};
         }
       }
 

@@ -167,11 +167,20 @@ __device__ __forceinline__ void combine_from(float& A, float& B) {
   A = pA * A;
 }
 
+// Lane movement in which lanes without a source read 0 (bound_ctrl), for values whose such
+// lanes are selected away afterwards: unlike dpp() it needs no `old` value moved into place
+// first, so it is one instruction instead of two.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_any(float src) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, src), kCtrl, 0xf, 0xf, true));
+}
+
 // Same, but lanes with !ok combine with the identity (segments narrower than a DPP row).
 template <int kCtrl>
 __device__ __forceinline__ void combine_from_masked(float& A, float& B, bool ok) {
-  float pA = dpp<kCtrl>(1.0f, A);
-  float pB = dpp<kCtrl>(0.0f, B);
+  float pA = dpp_any<kCtrl>(A);
+  float pB = dpp_any<kCtrl>(B);
   pA = ok ? pA : 1.0f;
   pB = ok ? pB : 0.0f;
   B = fmaf(pB, A, B);
