@@ -439,11 +439,11 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
   }
   __syncthreads();
   // The two steps before the loop issue what a steady-state step issues, in the same order
-  // (predecessor words, here out of range; the claim two steps ahead; the refill), so that
-  // the compiler's wait counts at the loop head are the steady-state ones. Otherwise the
-  // path into the loop makes it wait there for the words and the claim just issued.
-  uint64_t held_agg[kClAggs];
-  uint32_t held_end;
+  // (the stores, here out of range; wave 0's predecessor words and claim; the refill), so
+  // that the compiler's wait counts at the loop head are the steady-state ones. Otherwise the
+  // path into the loop makes it wait there for loads just issued.
+  uint64_t held_agg[kClAggs] = {};
+  uint32_t held_end = 0;
   ClTile<kMode> ring[N];
 #pragma unroll
   for (int i = 2; i < N; ++i) {  // filled at the end of the first steps
@@ -457,10 +457,16 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
+    end_store(st, kNoOffset, 0u);
+    status_store(st, kNoOffset, 0ull);
+    bst16(st, kNoOffset, u32x4{0u, 0u, 0u, 0u});
+    if constexpr (kMode == kBwd) bst16(st, kNoOffset, u32x4{0u, 0u, 0u, 0u});
+    if (w == 0) {
 #pragma unroll
-    for (int j = 0; j < kClAggs; ++j) held_agg[j] = status_load(st, kNoOffset);
-    held_end = end_load(st, kNoOffset);
-    pending[N - 2 + i] = claims.issue(st, leader && !claims_done);
+      for (int j = 0; j < kClAggs; ++j) held_agg[j] = status_load(st, kNoOffset);
+      held_end = end_load(st, kNoOffset);
+      pending[N - 2 + i] = claims.issue(st, leader && !claims_done);
+    }
     cl_tile_setup<E, kMode>(a, ring[i],
                             min(__builtin_amdgcn_readfirstlane(first_tiles[i]), ntiles),
                             __builtin_amdgcn_readfirstlane(first_grps[i]), ntiles, cg, w, c, r);
@@ -512,9 +518,12 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
         }
       }
 
-      // (2) the finishing tile's carry per column from its predecessors' words (wave 0; the
-      // other waves hold out-of-range words, zeros, and compute a carry nobody uses)
-      {
+      // (2) wave 0: the finishing tile's carry per column from its predecessors' words, and
+      // the tile's end values. The store is issued by every wave, out of range outside wave 0:
+      // a store inside a branch would leave the compiler unsure how many memory operations
+      // follow each load.
+      uint32_t end_off = kNoOffset, end_word = 0;
+      if (w == 0) {
         const int na = min(fin.seg, kClAggs);  // aggregates composed (uniform)
         if (__builtin_amdgcn_ballot_w64(agg_missing(held_agg, na) ||
                                         (fin.seg > kClAggs && held_end == kEndNotPublished)) != 0) {
@@ -562,18 +571,14 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
                          __uint_as_float((uint32_t)(word >> 32)));
           }
         }
-        // wave 0 hands the carries on and publishes the finishing tile's end values, which
-        // tile k+4 reads (the store is issued by every wave, out of range elsewhere: a store
-        // inside a branch would leave the compiler unsure how many memory operations follow
-        // each load)
-        if (w == 0) carry_in[lane] = carry;
+        // hand the carries on; the end values are read by tile k+4
+        carry_in[lane] = carry;
         const f32x2 agg = aggs[hs][lane];
-        const bool publish = w == 0 && fin_live && fin.seg + kClAggs + 1 < a.nseg;
-        end_store(st,
-                  publish ? ends_off + (uint32_t)((fin.tile * kClTileCols + lane) * sizeof(uint32_t))
-                          : kNoOffset,
-                  canonical_bits(fmaf(agg.x, carry, agg.y)));
+        if (fin_live && fin.seg + kClAggs + 1 < a.nseg)
+          end_off = ends_off + (uint32_t)((fin.tile * kClTileCols + lane) * sizeof(uint32_t));
+        end_word = canonical_bits(fmaf(agg.x, carry, agg.y));
       }
+      end_store(st, end_off, end_word);
       if (leader) {
         const int64_t t = claims_done ? kDone : claims.resolve(pending[(u + D) % N], kBubble, kDone);
         claims_done = t == kDone;
@@ -646,10 +651,11 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
       }
 
       // (6) wave 0: the predecessor words of the tile finished next step (the current one),
-      // loaded before the refill below (vector loads return in issue order)
-      {
+      // loaded before the refill below (vector loads return in issue order), and the claim
+      // (the leader's lane)
+      if (w == 0) {
         const ClTile<kMode>& nxt = ring[(u + 3) % N];
-        const bool mine = w == 0 && nxt.tile < ntiles;
+        const bool mine = nxt.tile < ntiles;
 #pragma unroll
         for (int j = 0; j < kClAggs; ++j) {
           const int64_t p = nxt.tile - (int64_t)(j + 1) * nxt.nch;
@@ -661,8 +667,8 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
         held_end = end_load(st, mine && nxt.seg > kClAggs
                                     ? ends_off + (uint32_t)((q * kClTileCols + lane) * sizeof(uint32_t))
                                     : kNoOffset);
+        pending[u] = claims.issue(st, leader && !claims_done);
       }
-      pending[u] = claims.issue(st, leader && !claims_done);
       // (7) refill the finished slot with the tile claimed two steps ago
       cl_tile_setup<E, kMode>(a, fin, claim < ntiles ? claim : ntiles, claim_grp, ntiles, cg, w,
                               c, r);
