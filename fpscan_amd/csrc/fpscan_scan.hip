@@ -795,6 +795,13 @@ constexpr int kTileDefer = 2;
 // MI355X: at 128 MiB per tensor streaming wins (fp32 B2 D256 L65536 forward 72 us against
 // 87), at 512 MiB tiling wins by 6 % (fp32 B8 D1024 L16384) and at 1-2 GiB by 8-10 %.
 constexpr int64_t kTiledMinBytes = 512ll << 20;
+// The fused backward moves 5 tensors per tile instead of 3, so the same fixed cost is a smaller
+// share, and the streaming backward slows down on long rows (one workgroup per row streaming
+// 128 KiB or more per tensor). There tiling wins from 256 MiB per tensor: bf16 B2 D1024 L65536
+// 227 us against 241, fp32 B3 D1024 L32768 341 against 363, while on 32-64 KiB rows of the
+// same size streaming still wins by 2-9 %.
+constexpr int64_t kTiledMinBytesBwdLongRows = 256ll << 20;
+constexpr int64_t kLongRowBytes = 128ll << 10;
 
 struct TilePlan {
   bool use;
@@ -803,15 +810,18 @@ struct TilePlan {
   size_t bytes;    // workspace: one status word per tile + overrun and tile counters
 };
 
-// The forward/reverse scan and the backward use the same plan.
-TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling) {
+// The forward/reverse scan and the backward use the same tile geometry; only the automatic
+// size threshold differs (`bwd`).
+TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling, bool bwd) {
   TilePlan t{false, 0, 0, 0};
   const int64_t sub = 64 * (16 / size);
   const int64_t nsub = seqlen / sub;
   if (tiling == 1 || nsub < kTileWaves) return t;
   t.tpr = (int)(nsub / kTileWaves);
   if (t.tpr > 64) return t;
-  if (tiling == 0 && rows * seqlen * size < kTiledMinBytes) return t;
+  const int64_t min_bytes =
+      bwd && seqlen * size >= kLongRowBytes ? kTiledMinBytesBwdLongRows : kTiledMinBytes;
+  if (tiling == 0 && rows * seqlen * size < min_bytes) return t;
   t.ntiles = rows * t.tpr;
   if ((t.ntiles + kStatusExtraWords) * (int64_t)sizeof(uint64_t) > INT32_MAX) return t;
   t.use = true;
@@ -925,7 +935,7 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   constexpr int kSub = 64 * V;
   const int L = a.seqlen;
   const TilePlan plan =
-      plan_tiles(a.rows, L, E::kSize, g_tiling.load(std::memory_order_relaxed));
+      plan_tiles(a.rows, L, E::kSize, g_tiling.load(std::memory_order_relaxed), kMode == kBwd);
   if (!Gp::kFused && plan.use && workspace != nullptr && ws_bytes >= plan.bytes) {
     const int st = run_tiled<E, kMode>(a, plan, workspace, stream,
                                        E::kSlot * 3 + kMode);
@@ -1095,7 +1105,7 @@ size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dt
     return 0;
   if (op != FPSCAN_OP_FWD && op != FPSCAN_OP_BWD) return 0;
   const TilePlan plan = plan_tiles(batch * dim, seqlen, size,
-                                   g_tiling.load(std::memory_order_relaxed));
+                                   g_tiling.load(std::memory_order_relaxed), op == FPSCAN_OP_BWD);
   return plan.use ? plan.bytes : 0;
 }
 

@@ -89,8 +89,10 @@ int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out,
                     int dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* Device workspace, in bytes, that the tiled path of fpscan_scan_fwd/fpscan_scan_bwd uses
- * for this problem; 0 when the problem takes the row-streaming path (which needs none).
+/* Device workspace, in bytes, that the tiled path of fpscan_scan_fwd (op FPSCAN_OP_FWD) or
+ * fpscan_scan_bwd (FPSCAN_OP_BWD) uses for this problem; 0 when the problem takes the
+ * row-streaming path (which needs none). The two can differ: the backward tiles from a
+ * smaller size on long rows.
  * No reference counterpart: the reference kernel keeps its carries in shared memory
  * (full_scan.cu:55-57). */
 size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype, int op);

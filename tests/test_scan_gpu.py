@@ -505,6 +505,32 @@ def test_tiled_and_streaming_paths_agree_and_default_is_tiled_when_large():
     check(tiled.reshape(8192, -1)[rows], oracle.scan_f64(gs, xs), torch.bfloat16, "tiled c4")
 
 
+def test_backward_tiles_long_rows_from_256_mib():
+    """bf16 B2 D1024 L65536 (256 MiB per tensor, 128 KiB rows): the automatic plan tiles the
+    backward but streams the forward. The automatic backward agrees with the streamed one and
+    with the oracle on sampled rows."""
+    lib = _abi()
+    assert lib.fpscan_workspace_bytes(2, 1024, 65536, 2, 1) > 0
+    assert lib.fpscan_workspace_bytes(2, 1024, 65536, 2, 0) == 0
+    g, x, go = _bench_inputs(2, 1024, 65536, torch.bfloat16, "mamba", seed=8)
+    y = fpscan_amd.scan_forward(g, x)
+    gg, gx = fpscan_amd.scan_backward(g, y, go)  # automatic: tiled
+    try:
+        ops.set_tiling(1)
+        gg_s, gx_s = fpscan_amd.scan_backward(g, y, go)
+    finally:
+        ops.set_tiling(0)
+    torch.cuda.synchronize()
+    assert oracle.normwise_error(gx, gx_s) < 2e-2
+    assert oracle.normwise_error(gg, gg_s) < 2e-2
+    rows = torch.linspace(0, 2047, 8).long()
+    gs = g.reshape(2048, -1)[rows].cpu()
+    ys, gos = y.reshape(2048, -1)[rows].cpu(), go.reshape(2048, -1)[rows].cpu()
+    gg_ref, gx_ref = oracle.scan_bwd_f64(gs, ys, gos)
+    check(gx.reshape(2048, -1)[rows], gx_ref, torch.bfloat16, "tiled bwd 256 MiB grad_tokens")
+    check(gg.reshape(2048, -1)[rows], gg_ref, torch.bfloat16, "tiled bwd 256 MiB grad_gates")
+
+
 # ------------------------------------------------------------------ padded strides (C ABI)
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("L", [64, 4096, 65536])
