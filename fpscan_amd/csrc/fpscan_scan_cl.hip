@@ -510,8 +510,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
 #pragma unroll
           for (int e = 0; e < V; ++e) pa[e] = 1.0f;
         }
-#pragma unroll
-        for (int e = 0; e < V; ++e) segment_scan<R>(pa[e], pb[e], r);
+        segment_scan_k<R>(pa, pb, r);
         if (r == R - 1) {
 #pragma unroll
           for (int e = 0; e < V; ++e) exch[w][c * V + e] = f32x2{pa[e], pb[e]};

@@ -187,6 +187,19 @@ __device__ __forceinline__ void combine_from_masked(float& A, float& B, bool ok)
   A = pA * A;
 }
 
+// (A, B) := (lane - 4's map) o (A, B) in DPP banks 1 and 3 (lanes 4-7 and 12-15 of each
+// row); lanes of banks 0 and 2 keep their map. This is the last step of a scan over aligned
+// 8-lane segments, whose lanes 4..7 are exactly those banks, so the bank mask does what a
+// per-lane select would: each half is one instruction with the lane movement folded in
+// (B first, from the old A). s_nop 1 gives the two wait states a DPP read of a VGPR written
+// by the previous VALU instruction needs.
+__device__ __forceinline__ void combine_shr4_upper_banks(float& A, float& B) {
+  asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:4 row_mask:0xf bank_mask:0xa"
+      : "+v"(B)
+      : "v"(A));
+  asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xa" : "+v"(A));
+}
+
 // Inclusive scan over all 64 lanes.
 __device__ __forceinline__ void wave_scan(float& A, float& B) {
   combine_from<kRowShr1>(A, B);
@@ -197,6 +210,67 @@ __device__ __forceinline__ void wave_scan(float& A, float& B) {
   combine_from<kRowBcast31, 0xc>(A, B);  // lane 31 -> rows 2 and 3
 }
 
+// One step of a scan over aligned segments of 8 lanes: lanes whose position in the segment is
+// below kShift keep their map, the others combine with the map kShift lanes down.
+// Each select takes the lane movement as its operand (VOP2 v_cndmask with DPP, VCC = the
+// lanes that keep theirs, a compile-time pattern; bound_ctrl makes row-start lanes read 0,
+// and those lanes select the identity anyway), so a step is 4 VALU instructions instead of
+// 6. s_nop 1 gives the two wait states a DPP read of a just-written VGPR needs. (For segments
+// of 4 lanes, fp32 in the channel-last tiles, the set-up measured no faster than the plain
+// masked combine, so those keep it.)
+#define FPSCAN_SEGMENT_STEP(MASK, SHIFT)                                                   \
+  "s_mov_b32 vcc_lo, " MASK "\n\t"                                                       \
+  "s_mov_b32 vcc_hi, " MASK "\n\t"                                                       \
+  "s_nop 1\n\t"                                                                          \
+  "v_cndmask_b32_dpp %0, %2, %4, vcc row_shr:" SHIFT                                    \
+  " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"                                          \
+  "v_cndmask_b32_dpp %1, %3, %5, vcc row_shr:" SHIFT " row_mask:0xf bank_mask:0xf bound_ctrl:1"
+template <int kShift>
+__device__ __forceinline__ void combine_segment_step(float& A, float& B) {
+  static_assert(kShift == 1 || kShift == 2, "masked DPP steps");
+  float pA, pB;
+  if constexpr (kShift == 1)
+    asm(FPSCAN_SEGMENT_STEP("0x01010101", "1")
+        : "=&v"(pA), "=&v"(pB) : "v"(A), "v"(B), "v"(1.0f), "v"(0.0f) : "vcc");
+  else
+    asm(FPSCAN_SEGMENT_STEP("0x03030303", "2")
+        : "=&v"(pA), "=&v"(pB) : "v"(A), "v"(B), "v"(1.0f), "v"(0.0f) : "vcc");
+  B = fmaf(pB, A, B);
+  A = pA * A;
+}
+#define FPSCAN_SEGMENT_STEP2(MASK, SHIFT)                                                  \
+  "s_mov_b32 vcc_lo, " MASK "\n\t"                                                       \
+  "s_mov_b32 vcc_hi, " MASK "\n\t"                                                       \
+  "s_nop 1\n\t"                                                                          \
+  "v_cndmask_b32_dpp %0, %4, %8, vcc row_shr:" SHIFT                                    \
+  " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"                                          \
+  "v_cndmask_b32_dpp %1, %5, %9, vcc row_shr:" SHIFT                                    \
+  " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"                                          \
+  "v_cndmask_b32_dpp %2, %6, %8, vcc row_shr:" SHIFT                                    \
+  " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"                                          \
+  "v_cndmask_b32_dpp %3, %7, %9, vcc row_shr:" SHIFT " row_mask:0xf bank_mask:0xf bound_ctrl:1"
+// combine_segment_step on two maps per lane at once: one VCC set-up for both.
+template <int kShift>
+__device__ __forceinline__ void combine_segment_step2(float& A0, float& B0, float& A1,
+                                                      float& B1) {
+  static_assert(kShift == 1 || kShift == 2, "masked DPP steps");
+  float pA0, pB0, pA1, pB1;
+  if constexpr (kShift == 1)
+    asm(FPSCAN_SEGMENT_STEP2("0x01010101", "1")
+        : "=&v"(pA0), "=&v"(pB0), "=&v"(pA1), "=&v"(pB1)
+        : "v"(A0), "v"(B0), "v"(A1), "v"(B1), "v"(1.0f), "v"(0.0f) : "vcc");
+  else
+    asm(FPSCAN_SEGMENT_STEP2("0x03030303", "2")
+        : "=&v"(pA0), "=&v"(pB0), "=&v"(pA1), "=&v"(pB1)
+        : "v"(A0), "v"(B0), "v"(A1), "v"(B1), "v"(1.0f), "v"(0.0f) : "vcc");
+  B0 = fmaf(pB0, A0, B0);
+  A0 = pA0 * A0;
+  B1 = fmaf(pB1, A1, B1);
+  A1 = pA1 * A1;
+}
+#undef FPSCAN_SEGMENT_STEP
+#undef FPSCAN_SEGMENT_STEP2
+
 // Inclusive scan inside aligned segments of G lanes (G in {2, 4, 8, 16, 32}); sl = lane % G.
 template <int G>
 __device__ __forceinline__ void segment_scan(float& A, float& B, int sl) {
@@ -206,10 +280,32 @@ __device__ __forceinline__ void segment_scan(float& A, float& B, int sl) {
     combine_from<kRowShr4>(A, B);
     combine_from<kRowShr8>(A, B);
     if constexpr (G == 32) combine_from<kRowBcast15, 0xa>(A, B);
+  } else if constexpr (G == 8) {
+    combine_segment_step<1>(A, B);
+    combine_segment_step<2>(A, B);
+    combine_shr4_upper_banks(A, B);
   } else {
     combine_from_masked<kRowShr1>(A, B, sl >= 1);
-    if constexpr (G >= 4) combine_from_masked<kRowShr2>(A, B, sl >= 2);
-    if constexpr (G == 8) combine_from_masked<kRowShr4>(A, B, sl >= 4);
+    if constexpr (G == 4) combine_from_masked<kRowShr2>(A, B, sl >= 2);
+  }
+}
+
+// segment_scan of K maps per lane (K even) over aligned segments of G lanes, sl = lane % G;
+// segments of 8 take the maps two at a time.
+template <int G, int K>
+__device__ __forceinline__ void segment_scan_k(float (&A)[K], float (&B)[K], int sl) {
+  static_assert(K % 2 == 0, "pairs of maps");
+#pragma unroll
+  for (int e = 0; e < K; e += 2) {
+    if constexpr (G == 8) {
+      combine_segment_step2<1>(A[e], B[e], A[e + 1], B[e + 1]);
+      combine_segment_step2<2>(A[e], B[e], A[e + 1], B[e + 1]);
+      combine_shr4_upper_banks(A[e], B[e]);
+      combine_shr4_upper_banks(A[e + 1], B[e + 1]);
+    } else {
+      segment_scan<G>(A[e], B[e], sl);
+      segment_scan<G>(A[e + 1], B[e + 1], sl);
+    }
   }
 }
 
