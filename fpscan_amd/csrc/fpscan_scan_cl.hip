@@ -595,10 +595,10 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
         const int col = 4 * w + (lane >> 4);
         const f32x2 e = exch[i][col];
         float eA = e.x, eB = e.y;
-        combine_from<kRowShr1>(eA, eB);
-        combine_from<kRowShr2>(eA, eB);
-        combine_from<kRowShr4>(eA, eB);
-        combine_from<kRowShr8>(eA, eB);
+        combine_from_row<1>(eA, eB);
+        combine_from_row<2>(eA, eB);
+        combine_from_row<4>(eA, eB);
+        combine_from_row<8>(eA, eB);
         if (i < 15) pref[i + 1][col] = f32x2{eA, eB};
         if (i == 15) aggs[hs][col] = f32x2{eA, eB};
         const bool publish = cur_live && i == 15;
