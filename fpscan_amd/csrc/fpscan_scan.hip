@@ -389,10 +389,10 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
             eA = t.x;
             eB = t.y;
           }
-          combine_from<kRowShr1>(eA, eB);
-          if constexpr (W > 2) combine_from<kRowShr2>(eA, eB);
-          if constexpr (W > 4) combine_from<kRowShr4>(eA, eB);
-          if constexpr (W > 8) combine_from<kRowShr8>(eA, eB);
+          combine_from_row<1>(eA, eB);
+          if constexpr (W > 2) combine_from_row<2>(eA, eB);
+          if constexpr (W > 4) combine_from_row<4>(eA, eB);
+          if constexpr (W > 8) combine_from_row<8>(eA, eB);
           if (w > 0) c_in = fmaf(readlane(eA, w - 1), carry, readlane(eB, w - 1));
           carry = fmaf(readlane(eA, W - 1), carry, readlane(eB, W - 1));
         }
@@ -620,10 +620,10 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
         eA = e.x;
         eB = e.y;
       }
-      combine_from<kRowShr1>(eA, eB);
-      if constexpr (TW > 2) combine_from<kRowShr2>(eA, eB);
-      if constexpr (TW > 4) combine_from<kRowShr4>(eA, eB);
-      if constexpr (TW > 8) combine_from<kRowShr8>(eA, eB);
+      combine_from_row<1>(eA, eB);
+      if constexpr (TW > 2) combine_from_row<2>(eA, eB);
+      if constexpr (TW > 4) combine_from_row<4>(eA, eB);
+      if constexpr (TW > 8) combine_from_row<8>(eA, eB);
       const float cur_pA = (w > 0) ? readlane(eA, w - 1) : 1.0f;
       const float cur_pB = (w > 0) ? readlane(eB, w - 1) : 0.0f;
       const bool publisher = cur_live && w == 0 && lane == 0;

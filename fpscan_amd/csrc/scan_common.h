@@ -200,12 +200,52 @@ __device__ __forceinline__ void combine_shr4_upper_banks(float& A, float& B) {
   asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xa" : "+v"(A));
 }
 
+// combine_from<row_shr:kShift> (full rows, lanes without a source keep their map) with the
+// lane movement folded into the arithmetic: B += B[lane - kShift] * A as one DPP
+// multiply-add whose missing sources read 0 (bound_ctrl), then A *= A[lane - kShift] as one
+// bank-masked DPP multiply (shifts 4 and 8: the lanes without a source are whole banks) or as
+// a DPP select of 1 for the first kShift lanes of each row plus a multiply (shifts 1 and 2).
+// 2-3 VALU instructions instead of 6. s_nop 1: a DPP read of a VGPR just written needs two
+// wait states.
+template <int kShift>
+__device__ __forceinline__ void combine_from_row(float& A, float& B) {
+  static_assert(kShift == 1 || kShift == 2 || kShift == 4 || kShift == 8, "row shifts");
+  if constexpr (kShift == 1)
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:1 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(B) : "v"(A));
+  else if constexpr (kShift == 2)
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:2 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(B) : "v"(A));
+  else if constexpr (kShift == 4)
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:4 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(B) : "v"(A));
+  else
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(B) : "v"(A));
+  if constexpr (kShift == 4) {
+    asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xe" : "+v"(A));
+  } else if constexpr (kShift == 8) {
+    asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xc" : "+v"(A));
+  } else {
+    float pA;
+    if constexpr (kShift == 1)
+      asm("s_mov_b32 vcc_lo, 0x00010001\n\ts_mov_b32 vcc_hi, 0x00010001\n\ts_nop 1\n\t"
+          "v_cndmask_b32_dpp %0, %1, %2, vcc row_shr:1 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+          : "=&v"(pA) : "v"(A), "v"(1.0f) : "vcc");
+    else
+      asm("s_mov_b32 vcc_lo, 0x00030003\n\ts_mov_b32 vcc_hi, 0x00030003\n\ts_nop 1\n\t"
+          "v_cndmask_b32_dpp %0, %1, %2, vcc row_shr:2 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+          : "=&v"(pA) : "v"(A), "v"(1.0f) : "vcc");
+    A = pA * A;
+  }
+}
+
 // Inclusive scan over all 64 lanes.
 __device__ __forceinline__ void wave_scan(float& A, float& B) {
-  combine_from<kRowShr1>(A, B);
-  combine_from<kRowShr2>(A, B);
-  combine_from<kRowShr4>(A, B);
-  combine_from<kRowShr8>(A, B);
+  combine_from_row<1>(A, B);
+  combine_from_row<2>(A, B);
+  combine_from_row<4>(A, B);
+  combine_from_row<8>(A, B);
   combine_from<kRowBcast15, 0xa>(A, B);  // lane 15 -> row 1, lane 47 -> row 3
   combine_from<kRowBcast31, 0xc>(A, B);  // lane 31 -> rows 2 and 3
 }
@@ -270,46 +310,6 @@ __device__ __forceinline__ void combine_segment_step2(float& A0, float& B0, floa
 }
 #undef FPSCAN_SEGMENT_STEP
 #undef FPSCAN_SEGMENT_STEP2
-
-// combine_from<row_shr:kShift> (full rows, lanes without a source keep their map) with the
-// lane movement folded into the arithmetic: B += B[lane - kShift] * A as one DPP
-// multiply-add whose missing sources read 0 (bound_ctrl), then A *= A[lane - kShift] as one
-// bank-masked DPP multiply (shifts 4 and 8: the lanes without a source are whole banks) or as
-// a DPP select of 1 for the first kShift lanes of each row plus a multiply (shifts 1 and 2).
-// 2-3 VALU instructions instead of 6. s_nop 1: a DPP read of a VGPR just written needs two
-// wait states.
-template <int kShift>
-__device__ __forceinline__ void combine_from_row(float& A, float& B) {
-  static_assert(kShift == 1 || kShift == 2 || kShift == 4 || kShift == 8, "row shifts");
-  if constexpr (kShift == 1)
-    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:1 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-        : "+v"(B) : "v"(A));
-  else if constexpr (kShift == 2)
-    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:2 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-        : "+v"(B) : "v"(A));
-  else if constexpr (kShift == 4)
-    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:4 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-        : "+v"(B) : "v"(A));
-  else
-    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-        : "+v"(B) : "v"(A));
-  if constexpr (kShift == 4) {
-    asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xe" : "+v"(A));
-  } else if constexpr (kShift == 8) {
-    asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xc" : "+v"(A));
-  } else {
-    float pA;
-    if constexpr (kShift == 1)
-      asm("s_mov_b32 vcc_lo, 0x00010001\n\ts_mov_b32 vcc_hi, 0x00010001\n\ts_nop 1\n\t"
-          "v_cndmask_b32_dpp %0, %1, %2, vcc row_shr:1 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-          : "=&v"(pA) : "v"(A), "v"(1.0f) : "vcc");
-    else
-      asm("s_mov_b32 vcc_lo, 0x00030003\n\ts_mov_b32 vcc_hi, 0x00030003\n\ts_nop 1\n\t"
-          "v_cndmask_b32_dpp %0, %1, %2, vcc row_shr:2 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-          : "=&v"(pA) : "v"(A), "v"(1.0f) : "vcc");
-    A = pA * A;
-  }
-}
 
 // Inclusive scan inside aligned segments of G lanes (G in {2, 4, 8, 16, 32}); sl = lane % G.
 template <int G>
