@@ -240,14 +240,28 @@ __device__ __forceinline__ void combine_from_row(float& A, float& B) {
   }
 }
 
+// The two cross-row steps of a wave scan, folded the same way: rows outside the row mask are
+// not written, which keeps their map. Row 1 takes lane 15's map and row 3 lane 47's
+// (row_bcast:15, rows 1 and 3); rows 2 and 3 take lane 31's (row_bcast:31, rows 2 and 3).
+__device__ __forceinline__ void combine_from_bcast15(float& A, float& B) {
+  asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_bcast:15 row_mask:0xa bank_mask:0xf"
+      : "+v"(B) : "v"(A));
+  asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf" : "+v"(A));
+}
+__device__ __forceinline__ void combine_from_bcast31(float& A, float& B) {
+  asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_bcast:31 row_mask:0xc bank_mask:0xf"
+      : "+v"(B) : "v"(A));
+  asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf" : "+v"(A));
+}
+
 // Inclusive scan over all 64 lanes.
 __device__ __forceinline__ void wave_scan(float& A, float& B) {
   combine_from_row<1>(A, B);
   combine_from_row<2>(A, B);
   combine_from_row<4>(A, B);
   combine_from_row<8>(A, B);
-  combine_from<kRowBcast15, 0xa>(A, B);  // lane 15 -> row 1, lane 47 -> row 3
-  combine_from<kRowBcast31, 0xc>(A, B);  // lane 31 -> rows 2 and 3
+  combine_from_bcast15(A, B);  // lane 15 -> row 1, lane 47 -> row 3
+  combine_from_bcast31(A, B);  // lane 31 -> rows 2 and 3
 }
 
 // One step of a scan over aligned segments of 8 lanes: lanes whose position in the segment is
