@@ -158,15 +158,6 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-// (A, B) := (earlier) o (A, B): the earlier lane's map is applied first.
-template <int kCtrl, int kRowMask = 0xf>
-__device__ __forceinline__ void combine_from(float& A, float& B) {
-  const float pA = dpp<kCtrl, kRowMask>(1.0f, A);
-  const float pB = dpp<kCtrl, kRowMask>(0.0f, B);
-  B = fmaf(pB, A, B);
-  A = pA * A;
-}
-
 // Lane movement in which lanes without a source read 0 (bound_ctrl), for values whose such
 // lanes are selected away afterwards: unlike dpp() it needs no `old` value moved into place
 // first, so it is one instruction instead of two.
@@ -176,7 +167,11 @@ __device__ __forceinline__ float dpp_any(float src) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, src), kCtrl, 0xf, 0xf, true));
 }
 
-// Same, but lanes with !ok combine with the identity (segments narrower than a DPP row).
+// Scan steps combine a lane's affine map (A, B) with an earlier lane's map (pA, pB), which is
+// applied first: (A, B) := (pA·A, pB·A + B). The identity is (1, 0).
+//
+// combine_from_masked: the earlier lane is kCtrl's DPP source; lanes with !ok combine with
+// the identity (segments narrower than a DPP row).
 template <int kCtrl>
 __device__ __forceinline__ void combine_from_masked(float& A, float& B, bool ok) {
   float pA = dpp_any<kCtrl>(A);
@@ -200,13 +195,14 @@ __device__ __forceinline__ void combine_shr4_upper_banks(float& A, float& B) {
   asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xa" : "+v"(A));
 }
 
-// combine_from<row_shr:kShift> (full rows, lanes without a source keep their map) with the
-// lane movement folded into the arithmetic: B += B[lane - kShift] * A as one DPP
-// multiply-add whose missing sources read 0 (bound_ctrl), then A *= A[lane - kShift] as one
-// bank-masked DPP multiply (shifts 4 and 8: the lanes without a source are whole banks) or as
-// a DPP select of 1 for the first kShift lanes of each row plus a multiply (shifts 1 and 2).
-// 2-3 VALU instructions instead of 6. s_nop 1: a DPP read of a VGPR just written needs two
-// wait states.
+// combine_from_row: the earlier lane is kShift lanes down in the same DPP row
+// (row_shr:kShift); the first kShift lanes of each row keep their map. The lane movement is
+// folded into the arithmetic: B += B[lane - kShift] * A as one DPP multiply-add whose missing
+// sources read 0 (bound_ctrl), then A *= A[lane - kShift] as one bank-masked DPP multiply
+// (shifts 4 and 8: the lanes without a source are whole banks) or as a DPP select of 1 for
+// the first kShift lanes of each row plus a multiply (shifts 1 and 2). 2-3 VALU instructions
+// instead of 6 (an identity moved into place, two lane moves, multiply-add, multiply).
+// s_nop 1: a DPP read of a VGPR just written needs two wait states.
 template <int kShift>
 __device__ __forceinline__ void combine_from_row(float& A, float& B) {
   static_assert(kShift == 1 || kShift == 2 || kShift == 4 || kShift == 8, "row shifts");
@@ -329,11 +325,11 @@ __device__ __forceinline__ void combine_segment_step2(float& A0, float& B0, floa
 template <int G>
 __device__ __forceinline__ void segment_scan(float& A, float& B, int sl) {
   if constexpr (G >= 16) {
-    combine_from<kRowShr1>(A, B);
-    combine_from<kRowShr2>(A, B);
-    combine_from<kRowShr4>(A, B);
-    combine_from<kRowShr8>(A, B);
-    if constexpr (G == 32) combine_from<kRowBcast15, 0xa>(A, B);
+    combine_from_row<1>(A, B);
+    combine_from_row<2>(A, B);
+    combine_from_row<4>(A, B);
+    combine_from_row<8>(A, B);
+    if constexpr (G == 32) combine_from_bcast15(A, B);
   } else if constexpr (G == 8) {
     combine_segment_step<1>(A, B);
     combine_segment_step<2>(A, B);
