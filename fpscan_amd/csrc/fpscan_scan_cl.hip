@@ -259,6 +259,10 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 //   4. the carry into the tile, per column, from its predecessors (below); each lane then
 //      has y = M(carry) for its V columns, with M its composed map, and stores;
 //   5. wave 0 publishes the tile's last value per column (a 32-bit word), y_end = A c + B.
+// The look-back below (its words, their composition, the polls and the claims) runs in wave
+// 0 only, under a wave-uniform branch; the other waves skip it. Only the end-value store is
+// issued by every wave, out of range outside wave 0, so that the compiler's count of
+// outstanding memory operations is the same on both sides of the branch.
 // Look-back: the predecessors of tile k are the earlier tiles of its chain, k-1, k-2, ...
 // The carry into k is always composed the same way, so results do not depend on timing:
 //     carry(k) = agg(k-1) o agg(k-2) o agg(k-3) applied to y_end(k-4)
