@@ -329,7 +329,7 @@ void fullscan_backward_softplus(const at::Tensor& z, const at::Tensor& rate,
 int set_launch_override(int waves_per_row, int ring_depth) {
   const int status = fpscan_set_launch_override(waves_per_row, ring_depth);
   TORCH_CHECK(status == FPSCAN_OK, "waves_per_row must be one of 0,1,2,4,8,16 and ring_depth "
-              "one of 0,1,2,4");
+              "one of 0..4");
   return status;
 }
 

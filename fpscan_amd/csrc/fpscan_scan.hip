@@ -869,8 +869,14 @@ const void* long_kernel(int u) {
   if constexpr (W == 1) {
     if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4, Gp>);
   }
-  // W > 1 keeps at most two sub-chunks in flight per wave: the W waves of a row already
-  // multiply the bytes in flight, and deeper rings exceed 64 VGPRs.
+  // W = 16 keeps three sub-chunks in flight per wave: measured 2-5 % faster than two on
+  // rows of 4 or more rounds (bf16 B8 D1024 L65536 forward 552 us against 568, backward 928
+  // against 972; the backward at 77 VGPRs then runs one workgroup per CU). Other W keep at
+  // most two: their waves already multiply the bytes in flight. So do fused gates: their
+  // backward at three spills registers (128 VGPRs, measured 35 % slower).
+  if constexpr (W == 16 && !Gp::kFused) {
+    if (u >= 3) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 3, Gp>);
+  }
   if (u >= 2) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 2, Gp>);
   return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 1, Gp>);
 }
@@ -953,7 +959,7 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   // controllers and address translation reward. Few-row problems also fill the device this
   // way (rows * 16 waves).
   int w = nsub < 16 ? nsub : 16;
-  int u_max = (w == 1 && kMode != kBwd) ? 4 : 2;
+  int u_max = (w == 1 && kMode != kBwd) ? 4 : (w == 16 && !Gp::kFused ? 3 : 2);
   const int ow = g_override_w.load(std::memory_order_relaxed);
   const int ou = g_override_u.load(std::memory_order_relaxed);
   if (ow > 0) w = ow <= nsub ? ow : nsub;
@@ -1135,7 +1141,7 @@ int fpscan_set_tiling(int mode) {
 int fpscan_set_launch_override(int waves_per_row, int ring_depth) {
   const bool w_ok = waves_per_row == 0 || waves_per_row == 1 || waves_per_row == 2 ||
                     waves_per_row == 4 || waves_per_row == 8 || waves_per_row == 16;
-  const bool u_ok = ring_depth == 0 || ring_depth == 1 || ring_depth == 2 || ring_depth == 4;
+  const bool u_ok = ring_depth >= 0 && ring_depth <= 4;
   if (!w_ok || !u_ok) return FPSCAN_ERR_SHAPE;
   g_override_w.store(waves_per_row, std::memory_order_relaxed);
   g_override_u.store(ring_depth, std::memory_order_relaxed);

@@ -187,7 +187,7 @@ const char* fpscan_strerror(int status);
 int fpscan_abi_version(void);
 
 /* Launch-shape override for tuning sweeps; process-wide, not synchronised with calls in
- * flight on other threads. waves_per_row in {0,1,2,4,8,16}, ring_depth in {0,1,2,4};
+ * flight on other threads. waves_per_row in {0,1,2,4,8,16}, ring_depth in 0..4;
  * 0 restores the built-in choice. Every setting computes the same recurrence; only the
  * grouping of fp32 partial products (and so the last-bit rounding) changes. The ring
  * depth never changes results. No reference counterpart: the

@@ -157,7 +157,8 @@ def test_null_pointer_rejected_and_empty_problem_accepted(lib):
 def test_launch_override_validation(lib):
     d = header_defines()
     assert lib.fpscan_set_launch_override(3, 0) == d["FPSCAN_ERR_SHAPE"]
-    assert lib.fpscan_set_launch_override(0, 3) == d["FPSCAN_ERR_SHAPE"]
+    assert lib.fpscan_set_launch_override(0, 5) == d["FPSCAN_ERR_SHAPE"]
+    assert lib.fpscan_set_launch_override(16, 3) == 0
     assert lib.fpscan_set_launch_override(4, 2) == 0
     assert lib.fpscan_set_launch_override(0, 0) == 0
 

@@ -250,7 +250,7 @@ def test_runs_on_the_current_stream():
     check(out, oracle.scan_f64(g, x), torch.float32, "side stream")
 
 
-@pytest.mark.parametrize("waves,ring", [(w, u) for w in (1, 2, 4, 8, 16) for u in (1, 2, 4)])
+@pytest.mark.parametrize("waves,ring", [(w, u) for w in (1, 2, 4, 8, 16) for u in (1, 2, 3, 4)])
 def test_every_launch_shape(waves, ring):
     """All (waves per row, ring depth) variants: exact on integer data, oracle-close on random
     data, forward, reverse and backward, every dtype."""
