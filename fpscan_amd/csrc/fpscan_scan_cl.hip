@@ -273,8 +273,10 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 // holding the lowest unfinished tile of a group always progresses (the row kernel's argument,
 // by induction over tile order). As in the row kernel, the words a finish needs are loaded
 // one step ahead (here right after the tile's reduce, kClDefer = 1) and only missing ones are
-// polled (bounded, device-coherent). With about 4 * kClBlocksPerChain tiles of a chain in
-// flight, tile k-4 has usually finished by then.
+// polled (bounded, device-coherent). The grid is every workgroup that fits on the device, so
+// with few chains many tiles of one chain are in flight and a finish often waits for y_end(k-4);
+// the finishes of a chain then follow each other at the publish latency, which still beats
+// cutting the time axis into segments (measured on MI355X down to one chain).
 //
 // Workspace: ntiles * 64 aggregate words (8 bytes; tile-major, one per column), ntiles * 64
 // end values (4 bytes), then the overrun word and claim counters as in the row kernel.
@@ -753,12 +755,12 @@ int launch_cl(const ClArgs& a, hipStream_t stream) {
   return err == hipSuccess ? FPSCAN_OK : FPSCAN_ERR_LAUNCH;
 }
 
-// Tiled path. It replaces the segments wherever one pass per strip lacks waves and there are
-// enough chains: the persistent grid is capped at kClBlocksPerChain workgroups per chain, so
-// that about 3 * kClBlocksPerChain tiles of a chain are in flight at once and the end value a
-// finishing tile needs (kClAggs + 1 tiles back) is usually published already.
-constexpr int64_t kClTileMinChains = 64;
-constexpr int64_t kClBlocksPerChain = 2;
+// Tiled path. It replaces the segments wherever one pass per strip lacks waves, whatever the
+// number of chains, with a persistent grid of every workgroup that fits on the device (at most
+// one per tile). Measured on MI355X, bf16 forward / backward, against the segments: (4, 65536,
+// 1024) 64 chains 341 / 478 us against 484 / 689; (1, 65536, 1024) 16 chains 128 / 166 against
+// 248 / 299; (1, 65536, 64) one chain 112 / 111 against 292 / 304. A cap of 2 workgroups per
+// chain cost 40-150 % below 128 chains.
 
 struct ClTilePlan {
   bool use;
@@ -787,7 +789,7 @@ ClTilePlan plan_cl_tiles(int64_t batch, int64_t seqlen, int64_t dim, int64_t str
   if ((steps + 2) * stride_t * size > INT32_MAX) return t;
   if (tiling == 0) {
     const int64_t strips = (dim + 64 * cl_vec(size) - 1) / (64 * cl_vec(size));
-    if (batch * strips >= kClMinTasks || t.chains < kClTileMinChains || t.nseg < 2) return t;
+    if (batch * strips >= kClMinTasks || t.nseg < 2) return t;
   }
   t.use = true;
   t.bytes = (size_t)words * sizeof(uint64_t);
@@ -835,7 +837,6 @@ int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t 
     return FPSCAN_ERR_LAUNCH;
   int64_t grid = resident;
   if (grid > ntiles) grid = ntiles;
-  if (grid > kClBlocksPerChain * plan.chains) grid = kClBlocksPerChain * plan.chains;
   a.chains = plan.chains;
   a.strips64 = plan.strips64;
   a.nseg = (int32_t)plan.nseg;

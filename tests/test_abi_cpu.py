@@ -248,23 +248,26 @@ def _cl_tiled_bytes(batch, seqlen, dim, itemsize):
 
 def test_channel_last_workspace_plan(cl_lib):
     """Automatic choice: one pass when batch x strips (64 16-byte vectors each) reaches 512;
-    below that, the tiled single pass when there are at least 64 chains (batch x 64-column
-    strips), else segments of about 1024 steps, more if needed for 1024 wave tasks, never
-    below 64 steps, with one (A, B) pair of 8 bytes per segment per column."""
+    below that, the tiled single pass (tiles of 64 columns by 16 x 16/itemsize steps) when
+    seqlen spans more than one tile, else segments of about 1024 steps, more if needed for
+    1024 wave tasks, never below 64 steps, with one (A, B) pair of 8 bytes per segment per
+    column."""
     w = cl_lib.fpscan_workspace_bytes_cl
     assert w(64, 1024, 8192, 8192, 0, 0) == 0  # 64 x 32 strips: one pass
     assert w(64, 256, 4096, 4096, 0, 0) == 0  # config 5 in channel-last form: 1024 strips
     assert w(16, 4096, 8192, 8192, 0, 0) == 0  # 512 strips
-    assert w(1, 100, 64, 64, 0, 0) == 0  # too short to cut (< 2 segments of 64)
+    assert w(1, 100, 64, 64, 0, 0) == _cl_tiled_bytes(1, 100, 64, 4)  # two 64-step tiles
     # bf16 (8, 65536, 1024): 16 strips, 128 chains -> tiled, 512 tiles of 128 steps per chain
     assert w(8, 65536, 1024, 1024, 2, 0) == _cl_tiled_bytes(8, 65536, 1024, 2) == 50332800
     assert w(8, 65536, 1024, 1024, 2, 1) == _cl_tiled_bytes(8, 65536, 1024, 2)
     # fp32 (4, 4096, 8192): 128 strips, 512 chains -> tiled (64-step tiles)
     assert w(4, 4096, 8192, 8192, 0, 0) == _cl_tiled_bytes(4, 4096, 8192, 4)
-    # bf16 (4, 8192, 512): 32 chains -> 128 segments of 64 steps (capped by seqlen / 64)
-    assert w(4, 8192, 512, 512, 2, 0) == 128 * 4 * 512 * 8
-    # capped by seqlen / 64 segments: fp32 (1, 1000, 64) -> 15 segments of 67 steps
-    assert w(1, 1000, 64, 64, 0, 0) == 15 * 1 * 64 * 8
+    # few chains: bf16 (4, 8192, 512) 32 chains of 64 tiles, fp32 (1, 1000, 64) one of 16
+    assert w(4, 8192, 512, 512, 2, 0) == _cl_tiled_bytes(4, 8192, 512, 2) == 32 * 64 * 768 + 1152
+    assert w(1, 1000, 64, 64, 0, 0) == _cl_tiled_bytes(1, 1000, 64, 4) == 16 * 768 + 1152
+    # seqlen within one tile: bf16 (1, 128, 64) -> 2 segments of 64 steps (seqlen / 64)
+    assert w(1, 128, 64, 64, 2, 0) == 2 * 1 * 64 * 8
+    assert w(1, 64, 64, 64, 0, 0) == 0  # fp32, one tile and too short to cut: one pass
     assert w(1, 100, 64, 64, 0, 7) == 0  # unknown op
     assert w(1, 100, 64, 64, 5, 0) == 0  # unknown dtype
     assert w(1, 100, 64, 32, 0, 0) == 0  # stride_t < dim
@@ -278,6 +281,10 @@ def test_channel_last_workspace_plan_forced_modes(cl_lib):
         assert cl_lib.fpscan_set_tiling(1) == 0
         assert w(8, 65536, 1024, 1024, 2, 0) == 64 * 8 * 1024 * 8  # 64 segments of 1024
         assert w(4, 4096, 8192, 8192, 0, 0) == 8 * 4 * 8192 * 8  # 8 segments of 512
+        # segments capped by seqlen / 64: bf16 (4, 8192, 512) -> 128 of 64 steps,
+        # fp32 (1, 1000, 64) -> 15 of 67 steps
+        assert w(4, 8192, 512, 512, 2, 0) == 128 * 4 * 512 * 8
+        assert w(1, 1000, 64, 64, 0, 0) == 15 * 1 * 64 * 8
         assert w(64, 256, 4096, 4096, 0, 0) == 0
         assert cl_lib.fpscan_set_tiling(2) == 0
         assert w(1, 1000, 64, 64, 0, 0) == _cl_tiled_bytes(1, 1000, 64, 4) == 16 * 768 + 1152

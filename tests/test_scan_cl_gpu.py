@@ -7,12 +7,15 @@ pscan. So besides the oracle, every result is also compared with the row-major H
 transposed tensors: within the north-star tolerance on random data, and bit for bit on integer
 data, where every partial result is exact in any association order.
 
-Covered: forward, reverse and the fused backward in every dtype; the one-pass and the
-segmented (aggregate, carry, apply) paths, forced both ways through the C ABI; ragged and
+Covered: forward, reverse and the fused backward in every dtype; the automatic choice (which
+takes the tiled look-back, tests/test_scan_cl_tiled_gpu.py, wherever one pass per strip lacks
+strips), the one-pass and the segmented (aggregate, carry, apply) paths, the last two forced
+through the C ABI with the tiled look-back switched off (fpscan_set_tiling(1)); ragged and
 non-power-of-two shapes, seqlen 1, partial strips, empty tensors, in-place use, the ignored
 first gate, validation errors, autograd, and the channel-last forms of BASELINE configs 4 and
 5 at their real shapes.
 """
+import contextlib
 import ctypes
 import os
 
@@ -22,6 +25,7 @@ import torch
 
 import fpscan_amd
 import oracle
+from fpscan_amd.ops import set_tiling
 from scan_helpers import DEVICE, DTYPES, NORM_TOL, bits_equal, check
 
 pytestmark = [
@@ -44,6 +48,16 @@ def to_rows(t):
     return t.transpose(1, 2).contiguous()
 
 
+@contextlib.contextmanager
+def tiling(mode):
+    """fpscan_set_tiling(mode) for the block (process-wide), automatic again afterwards."""
+    set_tiling(mode)
+    try:
+        yield
+    finally:
+        set_tiling(0)
+
+
 @pytest.fixture(scope="module")
 def lib():
     lib = ctypes.CDLL(os.path.join(os.path.dirname(fpscan_amd.__file__), "libfpscan_hip.so"))
@@ -58,14 +72,17 @@ def lib():
 
 
 def abi_fwd(lib, g, x, reverse, segmented):
-    """The C ABI with (segmented) or without (one pass per strip) the workspace."""
+    """The C ABI with (segmented, the tiled look-back off) or without (one pass per strip) the
+    workspace."""
     B, L, D = x.shape
     out = torch.empty_like(x)
-    nbytes = lib.fpscan_workspace_bytes_cl(B, L, D, D, _CODE[x.dtype], 0) if segmented else 0
-    ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
-    st = lib.fpscan_scan_fwd_cl(g.data_ptr(), x.data_ptr(), out.data_ptr(), B, L, D, L * D, D,
-                                _CODE[x.dtype], int(reverse), ws.data_ptr() if nbytes else None,
-                                nbytes, torch.cuda.current_stream().cuda_stream)
+    with tiling(1):
+        nbytes = lib.fpscan_workspace_bytes_cl(B, L, D, D, _CODE[x.dtype], 0) if segmented else 0
+        ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
+        st = lib.fpscan_scan_fwd_cl(g.data_ptr(), x.data_ptr(), out.data_ptr(), B, L, D, L * D,
+                                    D, _CODE[x.dtype], int(reverse),
+                                    ws.data_ptr() if nbytes else None, nbytes,
+                                    torch.cuda.current_stream().cuda_stream)
     assert st == 0
     return out, nbytes
 
@@ -73,12 +90,13 @@ def abi_fwd(lib, g, x, reverse, segmented):
 def abi_bwd(lib, g, y, go, segmented):
     B, L, D = g.shape
     gg, gx = torch.empty_like(g), torch.empty_like(g)
-    nbytes = lib.fpscan_workspace_bytes_cl(B, L, D, D, _CODE[g.dtype], 1) if segmented else 0
-    ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
-    st = lib.fpscan_scan_bwd_cl(g.data_ptr(), y.data_ptr(), go.data_ptr(), gg.data_ptr(),
-                                gx.data_ptr(), B, L, D, L * D, D, _CODE[g.dtype],
-                                ws.data_ptr() if nbytes else None, nbytes,
-                                torch.cuda.current_stream().cuda_stream)
+    with tiling(1):
+        nbytes = lib.fpscan_workspace_bytes_cl(B, L, D, D, _CODE[g.dtype], 1) if segmented else 0
+        ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=DEVICE)
+        st = lib.fpscan_scan_bwd_cl(g.data_ptr(), y.data_ptr(), go.data_ptr(), gg.data_ptr(),
+                                    gx.data_ptr(), B, L, D, L * D, D, _CODE[g.dtype],
+                                    ws.data_ptr() if nbytes else None, nbytes,
+                                    torch.cuda.current_stream().cuda_stream)
     assert st == 0
     return gg, gx, nbytes
 
@@ -87,31 +105,36 @@ SHAPES = [
     (2, 64, 64),      # partial strip (64 of 256/512 columns), one pass
     (3, 1000, 40),    # seqlen not a power of two, dim not a multiple of a strip
     (1, 1, 256),      # one time step
-    (4, 300, 520),    # segmented, ragged last segment
-    (2, 4096, 1024),  # segmented, several strips
-    (1, 65536, 64),   # long and narrow: many segments
+    (4, 300, 520),    # tiled or segmented, ragged last tile or segment
+    (2, 4096, 1024),  # tiled or segmented, several strips
+    (1, 65536, 64),   # long and narrow: one chain of many tiles, or many segments
 ]
+PATHS = {"auto": 0, "no-tiles": 1}  # fpscan_set_tiling modes
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("shape", SHAPES, ids=str)
-def test_forward_and_reverse_match_oracle(dtype, shape):
+@pytest.mark.parametrize("path", PATHS)
+def test_forward_and_reverse_match_oracle(path, dtype, shape):
     g, x = cl_inputs(*shape, dtype, seed=sum(shape))
     gd, xd = g.to(DEVICE), x.to(DEVICE)
     for rev in (False, True):
-        out = fpscan_amd.scan_forward_channel_last(gd, xd, reverse=rev)
+        with tiling(PATHS[path]):
+            out = fpscan_amd.scan_forward_channel_last(gd, xd, reverse=rev)
         assert out.shape == x.shape and out.dtype == dtype
         check(out, oracle.scan_f64_channel_last(g, x, rev), dtype, f"cl {shape} rev={rev}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("shape", SHAPES, ids=str)
-def test_backward_matches_oracle(dtype, shape):
+@pytest.mark.parametrize("path", PATHS)
+def test_backward_matches_oracle(path, dtype, shape):
     g, x = cl_inputs(*shape, dtype, seed=sum(shape) + 1)
     go = torch.randn(shape, generator=torch.Generator().manual_seed(3)).to(dtype)
     gd = g.to(DEVICE)
-    y = fpscan_amd.scan_forward_channel_last(gd, x.to(DEVICE))
-    gg, gx = fpscan_amd.scan_backward_channel_last(gd, y, go.to(DEVICE))
+    with tiling(PATHS[path]):
+        y = fpscan_amd.scan_forward_channel_last(gd, x.to(DEVICE))
+        gg, gx = fpscan_amd.scan_backward_channel_last(gd, y, go.to(DEVICE))
     gg_ref, gx_ref = oracle.scan_bwd_f64_channel_last(g, y.cpu(), go)
     check(gx, gx_ref, dtype, f"cl {shape} grad_tokens")
     check(gg, gg_ref, dtype, f"cl {shape} grad_gates")
@@ -119,7 +142,7 @@ def test_backward_matches_oracle(dtype, shape):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 def test_one_pass_and_segmented_paths_match_oracle(lib, dtype):
-    shape = (2, 2048, 256)  # 2-4 strips in all: segmented by default
+    shape = (2, 2048, 256)  # 2-4 strips in all: segmented when the tiled look-back is off
     g, x = cl_inputs(*shape, dtype, seed=11)
     gd, xd = g.to(DEVICE), x.to(DEVICE)
     go = torch.randn(shape, generator=torch.Generator().manual_seed(4)).to(dtype)
@@ -260,7 +283,7 @@ def test_config4_channel_last_b8_l65536_d1024(dtype):
     g, x, go = to_rows(gr), to_rows(xr), to_rows(gor)
     del gr, xr, gor
     out = fpscan_amd.scan_forward_channel_last(g, x)
-    # reverse == flip(forward(flip)) bit for bit: the segments divide seqlen evenly, so the
+    # reverse == flip(forward(flip)) bit for bit: the tiles divide seqlen evenly, so the
     # reverse pass runs exactly the mirrored operations
     rev = fpscan_amd.scan_forward_channel_last(g, x, reverse=True)
     fwd_of_flip = fpscan_amd.scan_forward_channel_last(g.flip(1).contiguous(),
@@ -300,14 +323,15 @@ def test_padded_strides_through_the_c_abi(lib, dtype, segmented):
     outb, ggb, gxb = (embed(torch.zeros_like(x), -3.0) for _ in range(3))
     code = _CODE[dtype]
     stream = torch.cuda.current_stream().cuda_stream
-    nb = lib.fpscan_workspace_bytes_cl(B, L, D, st, code, 0) if segmented else 0
-    ws = torch.empty(max(nb, 8), dtype=torch.uint8, device=DEVICE)
-    assert (nb > 0) == segmented
-    assert lib.fpscan_scan_fwd_cl(gb.data_ptr(), xb.data_ptr(), outb.data_ptr(), B, L, D, sb, st,
-                                  code, 0, ws.data_ptr() if nb else None, nb, stream) == 0
-    assert lib.fpscan_scan_bwd_cl(gb.data_ptr(), outb.data_ptr(), gob.data_ptr(), ggb.data_ptr(),
-                                  gxb.data_ptr(), B, L, D, sb, st, code,
-                                  ws.data_ptr() if nb else None, nb, stream) == 0
+    with tiling(1):
+        nb = lib.fpscan_workspace_bytes_cl(B, L, D, st, code, 0) if segmented else 0
+        ws = torch.empty(max(nb, 8), dtype=torch.uint8, device=DEVICE)
+        assert (nb > 0) == segmented
+        assert lib.fpscan_scan_fwd_cl(gb.data_ptr(), xb.data_ptr(), outb.data_ptr(), B, L, D, sb,
+                                      st, code, 0, ws.data_ptr() if nb else None, nb, stream) == 0
+        assert lib.fpscan_scan_bwd_cl(gb.data_ptr(), outb.data_ptr(), gob.data_ptr(),
+                                      ggb.data_ptr(), gxb.data_ptr(), B, L, D, sb, st, code,
+                                      ws.data_ptr() if nb else None, nb, stream) == 0
     torch.cuda.synchronize()
     out = view(outb).cpu()
     check(out, oracle.scan_f64_channel_last(g, x), dtype, "cl strided fwd")

@@ -4,7 +4,8 @@ in fp32), against the CPU oracle (oracle.scan_f64_channel_last / scan_bwd_f64_ch
 pinned by tests/test_oracle.py).
 
 fpscan_set_tiling(2) forces the tiled path on every shape here; the automatic choice takes it
-only with at least 64 chains and too few strips for one pass. Besides the oracle: the
+wherever there are too few strips for one pass and more than one tile of steps. Besides the
+oracle: the
 workspace after a call (every tile's aggregate published, no wait overrun, claim counters at
 or past their group sizes), bit-exactness on integer data, run-to-run determinism and the
 reverse = flip(forward(flip)) identity bit for bit (the carry into a tile is always composed
