@@ -404,7 +404,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
 
   __shared__ f32x2 exch[kClTileWaves][kClTileCols + kPad];  // wave totals
   __shared__ f32x2 pref[kClTileWaves][kClTileCols + kPad];  // prefix entering each wave
-  __shared__ f32x2 aggs[D][kClTileCols];                    // tile aggregates, by deferral slot
+  __shared__ f32x2 aggs[N][kClTileCols];                    // tile aggregates, by ring slot
   __shared__ float carry_in[kClTileCols];
   __shared__ int64_t claimed;
   __shared__ int claimed_grp;
@@ -463,8 +463,8 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    end_store(st, kNoOffset, 0u);
     status_store(st, kNoOffset, 0ull);
+    end_store(st, kNoOffset, 0u);
     bst16(st, kNoOffset, u32x4{0u, 0u, 0u, 0u});
     if constexpr (kMode == kBwd) bst16(st, kNoOffset, u32x4{0u, 0u, 0u, 0u});
     if (w == 0) {
@@ -523,7 +523,31 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
         }
       }
 
-      // (2) wave 0: the finishing tile's carry per column from its predecessors' words, and
+      lds_barrier();
+
+      // (2) the current tile's wave prefixes and aggregate (wave w: columns 4w..4w+3). The
+      // aggregate is published before wave 0 waits for the finishing tile's predecessors, so
+      // that no wait delays a publication: with many tiles of a chain in flight, a successor's
+      // finish needs this word within the same step.
+      {
+        const int i = lane & 15;
+        const int col = 4 * w + (lane >> 4);
+        const f32x2 e = exch[i][col];
+        float eA = e.x, eB = e.y;
+        combine_from_row<1>(eA, eB);
+        combine_from_row<2>(eA, eB);
+        combine_from_row<4>(eA, eB);
+        combine_from_row<8>(eA, eB);
+        if (i < 15) pref[i + 1][col] = f32x2{eA, eB};
+        if (i == 15) aggs[u][col] = f32x2{eA, eB};
+        const bool publish = cur_live && i == 15;
+        status_store(st,
+                     publish ? (uint32_t)((cur.tile * kClTileCols + col) * sizeof(uint64_t))
+                             : kNoOffset,
+                     pack_map(eA, eB));
+      }
+
+      // (3) wave 0: the finishing tile's carry per column from its predecessors' words, and
       // the tile's end values. The store is issued by every wave, out of range outside wave 0:
       // a store inside a branch would leave the compiler unsure how many memory operations
       // follow each load.
@@ -578,7 +602,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
         }
         // hand the carries on; the end values are read by tile k+4
         carry_in[lane] = carry;
-        const f32x2 agg = aggs[hs][lane];
+        const f32x2 agg = aggs[(u + 2) % N][lane];
         if (fin_live && fin.seg + kClAggs + 1 < a.nseg)
           end_off = ends_off + (uint32_t)((fin.tile * kClTileCols + lane) * sizeof(uint32_t));
         end_word = canonical_bits(fmaf(agg.x, carry, agg.y));
@@ -594,25 +618,6 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
       const int64_t claim = __builtin_amdgcn_readfirstlane(claimed);
       const int claim_grp = __builtin_amdgcn_readfirstlane(claimed_grp);
       all_claimed = claim == kDone;
-
-      // (3) the current tile's wave prefixes and aggregate (wave w: columns 4w..4w+3)
-      {
-        const int i = lane & 15;
-        const int col = 4 * w + (lane >> 4);
-        const f32x2 e = exch[i][col];
-        float eA = e.x, eB = e.y;
-        combine_from_row<1>(eA, eB);
-        combine_from_row<2>(eA, eB);
-        combine_from_row<4>(eA, eB);
-        combine_from_row<8>(eA, eB);
-        if (i < 15) pref[i + 1][col] = f32x2{eA, eB};
-        if (i == 15) aggs[hs][col] = f32x2{eA, eB};
-        const bool publish = cur_live && i == 15;
-        status_store(st,
-                     publish ? (uint32_t)((cur.tile * kClTileCols + col) * sizeof(uint64_t))
-                             : kNoOffset,
-                     pack_map(eA, eB));
-      }
 
       // (4) finish the oldest deferred tile
       {
@@ -630,7 +635,6 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
           bst16(out1, fin.off, E::pack(o1));
         }
       }
-      lds_barrier();
 
       // (5) the current tile's composed maps, held until its finish
       {
