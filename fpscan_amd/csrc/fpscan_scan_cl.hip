@@ -265,18 +265,19 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 // outstanding memory operations is the same on both sides of the branch.
 // Look-back: the predecessors of tile k are the earlier tiles of its chain, k-1, k-2, ...
 // The carry into k is always composed the same way, so results do not depend on timing:
-//     carry(k) = agg(k-1) o agg(k-2) o agg(k-3) applied to y_end(k-4)
-// (fewer maps and the zero state near the chain start). Tiles are claimed in order (Claims
-// over chain groups: within a group all chains' tile 0, then all chains' tile 1, ...), so a
-// tile's predecessors were claimed before it. An aggregate is published by a reduce, which
-// never waits; y_end(k-4) by a finish, which waits only for earlier tiles. So the workgroup
-// holding the lowest unfinished tile of a group always progresses (the row kernel's argument,
-// by induction over tile order). As in the row kernel, the words a finish needs are loaded
-// one step ahead (here right after the tile's reduce, kClDefer = 1) and only missing ones are
-// polled (bounded, device-coherent). The grid is every workgroup that fits on the device, so
-// with few chains many tiles of one chain are in flight and a finish often waits for y_end(k-4);
-// the finishes of a chain then follow each other at the publish latency, which still beats
-// cutting the time axis into segments (measured on MI355X down to one chain).
+//     carry(k) = agg(k-1) o ... o agg(k-K) applied to y_end(k-K-1)
+// (fewer maps and the zero state near the chain start; K = 3 or 5, fixed by the shape).
+// Tiles are claimed in order (Claims over chain groups: within a group all chains' tile 0,
+// then all chains' tile 1, ...), so a tile's predecessors were claimed before it. An
+// aggregate is published by a reduce, which never waits; y_end(k-K-1) by a finish, which
+// waits only for earlier tiles. So the workgroup holding the lowest unfinished tile of a
+// group always progresses (the row kernel's argument, by induction over tile order). As in
+// the row kernel, the words a finish needs are loaded one step ahead (here right after the
+// tile's reduce, kClDefer = 1) and only missing ones are polled (bounded, device-coherent).
+// The grid is every workgroup that fits on the device, so with few chains many tiles of one
+// chain are in flight and a finish often waits for y_end(k-K-1): the finishes of a chain then
+// advance K+1 tiles per publish round trip, which still beats cutting the time axis into
+// segments (measured on MI355X down to one chain).
 //
 // Workspace: ntiles * 64 aggregate words (8 bytes; tile-major, one per column), ntiles * 64
 // end values (4 bytes), then the overrun word and claim counters as in the row kernel.
@@ -285,7 +286,17 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 constexpr int kClTileWaves = 16;
 constexpr int kClTileCols = 64;  // columns per chain and tile
 constexpr int kClDefer = 1;      // steps between a tile's reduce and its finish
-constexpr int kClAggs = 3;       // aggregates composed onto a predecessor's end value
+// Aggregates composed onto a predecessor's end value (the look-back depth K, a template
+// parameter of the kernel): 3 with at least kClShallowMinChains chains, where about 2 tiles of
+// a chain are in flight and end(k-4) is almost always published; 5 with fewer chains, where
+// many tiles of a chain are in flight and a finish would otherwise wait for end(k-4) within
+// the same step. Measured on MI355X (bf16 fwd / bwd, us): (2, 65536, 1024), 32 chains,
+// 210 / 276 with 3 against 197 / 270 with 5; fp32 (4, 65536, 1024), 64 chains, 579 / 909
+// against 550 / 909; (8, 65536, 1024), 128 chains, 600 / 937 against 612 / 918. 7 spills
+// registers in the half-type backward.
+constexpr int kClAggsShallow = 3;
+constexpr int kClAggsDeep = 5;
+constexpr int64_t kClShallowMinChains = 128;
 static_assert(kClTileWaves * 4 == kClTileCols, "wave w scans the totals of columns 4w..4w+3");
 
 constexpr uint32_t kEndNotPublished = ~0u;
@@ -392,7 +403,7 @@ __device__ __forceinline__ void cl_tile_setup(const ClArgs& a, ClTile<kMode>& ts
   }
 }
 
-template <class E, int kMode, int D>
+template <class E, int kMode, int D, int K>
 __global__ void __launch_bounds__(64 * kClTileWaves)
 scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntiles) {
   constexpr int V = E::V;
@@ -448,7 +459,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
   // (the stores, here out of range; wave 0's predecessor words and claim; the refill), so
   // that the compiler's wait counts at the loop head are the steady-state ones. Otherwise the
   // path into the loop makes it wait there for loads just issued.
-  uint64_t held_agg[kClAggs] = {};
+  uint64_t held_agg[K] = {};
   uint32_t held_end = 0;
   ClTile<kMode> ring[N];
 #pragma unroll
@@ -469,7 +480,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
     if constexpr (kMode == kBwd) bst16(st, kNoOffset, u32x4{0u, 0u, 0u, 0u});
     if (w == 0) {
 #pragma unroll
-      for (int j = 0; j < kClAggs; ++j) held_agg[j] = status_load(st, kNoOffset);
+      for (int j = 0; j < K; ++j) held_agg[j] = status_load(st, kNoOffset);
       held_end = end_load(st, kNoOffset);
       pending[N - 2 + i] = claims.issue(st, leader && !claims_done);
     }
@@ -553,9 +564,9 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
       // follow each load.
       uint32_t end_off = kNoOffset, end_word = 0;
       if (w == 0) {
-        const int na = min(fin.seg, kClAggs);  // aggregates composed (uniform)
+        const int na = min(fin.seg, K);  // aggregates composed (uniform)
         if (__builtin_amdgcn_ballot_w64(agg_missing(held_agg, na) ||
-                                        (fin.seg > kClAggs && held_end == kEndNotPublished)) != 0) {
+                                        (fin.seg > K && held_end == kEndNotPublished)) != 0) {
           // a predecessor has not published yet: poll the missing words (bounded; once any
           // wait of this launch has overrun, which a correct launch never does, the others
           // give up at once, so that the launch still ends soon)
@@ -564,19 +575,19 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
           for (int it = overran ? kSpinLimit : 0;; ++it) {
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-            for (int j = 0; j < kClAggs; ++j) {
+            for (int j = 0; j < K; ++j) {
               if (j < na && held_agg[j] == kNotPublished)
                 held_agg[j] = __hip_atomic_load(
                     status + (fin.tile - (int64_t)(j + 1) * fin.nch) * kClTileCols + lane,
                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (fin.seg > kClAggs && held_end == kEndNotPublished)
+            if (fin.seg > K && held_end == kEndNotPublished)
               held_end = __hip_atomic_load(
                   reinterpret_cast<const uint32_t*>(status + nagg) +
-                      (fin.tile - (int64_t)(kClAggs + 1) * fin.nch) * kClTileCols + lane,
+                      (fin.tile - (int64_t)(K + 1) * fin.nch) * kClTileCols + lane,
                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (__builtin_amdgcn_ballot_w64(agg_missing(held_agg, na) ||
-                                            (fin.seg > kClAggs && held_end == kEndNotPublished)) == 0)
+                                            (fin.seg > K && held_end == kEndNotPublished)) == 0)
               break;
             if (it == kSpinLimit) {
               if (lane == 0)
@@ -586,24 +597,24 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
             }
           }
 #pragma unroll
-          for (int j = 0; j < kClAggs; ++j)
+          for (int j = 0; j < K; ++j)
             held_agg[j] = held_agg[j] == kNotPublished ? 0ull : held_agg[j];
           held_end = held_end == kEndNotPublished ? 0u : held_end;
         }
         // carry = agg(k-1) o ... o agg(k-na) applied to y_end(k-na-1), or to the zero state
-        float carry = fin.seg > kClAggs ? __uint_as_float(held_end) : 0.0f;
+        float carry = fin.seg > K ? __uint_as_float(held_end) : 0.0f;
 #pragma unroll
-        for (int j = kClAggs - 1; j >= 0; --j) {
+        for (int j = K - 1; j >= 0; --j) {
           if (j < na) {
             const uint64_t word = held_agg[j];
             carry = fmaf(__uint_as_float((uint32_t)word), carry,
                          __uint_as_float((uint32_t)(word >> 32)));
           }
         }
-        // hand the carries on; the end values are read by tile k+4
+        // hand the carries on; the end values are read by tile k+K+1
         carry_in[lane] = carry;
         const f32x2 agg = aggs[(u + 2) % N][lane];
-        if (fin_live && fin.seg + kClAggs + 1 < a.nseg)
+        if (fin_live && fin.seg + K + 1 < a.nseg)
           end_off = ends_off + (uint32_t)((fin.tile * kClTileCols + lane) * sizeof(uint32_t));
         end_word = canonical_bits(fmaf(agg.x, carry, agg.y));
       }
@@ -666,14 +677,14 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
         const ClTile<kMode>& nxt = ring[(u + 3) % N];
         const bool mine = nxt.tile < ntiles;
 #pragma unroll
-        for (int j = 0; j < kClAggs; ++j) {
+        for (int j = 0; j < K; ++j) {
           const int64_t p = nxt.tile - (int64_t)(j + 1) * nxt.nch;
           held_agg[j] = status_load(
               st, mine && j < nxt.seg ? (uint32_t)((p * kClTileCols + lane) * sizeof(uint64_t))
                                       : kNoOffset);
         }
-        const int64_t q = nxt.tile - (int64_t)(kClAggs + 1) * nxt.nch;
-        held_end = end_load(st, mine && nxt.seg > kClAggs
+        const int64_t q = nxt.tile - (int64_t)(K + 1) * nxt.nch;
+        held_end = end_load(st, mine && nxt.seg > K
                                     ? ends_off + (uint32_t)((q * kClTileCols + lane) * sizeof(uint32_t))
                                     : kNoOffset);
         pending[u] = claims.issue(st, leader && !claims_done);
@@ -801,7 +812,7 @@ ClTilePlan plan_cl_tiles(int64_t batch, int64_t seqlen, int64_t dim, int64_t str
 }
 
 constexpr int kClMaxDevices = 64;
-std::atomic<int> g_cl_resident[kClMaxDevices][9];
+std::atomic<int> g_cl_resident[kClMaxDevices][18];  // 3 types x 3 modes x 2 look-back depths
 
 // Workgroups of `kernel` resident at once on the current device (CUs x blocks per CU), cached
 // per device and kernel; 0 if the device cannot be queried.
@@ -826,9 +837,13 @@ int cl_resident_blocks(const void* kernel, int slot, int threads) {
 // fails (the caller then takes another path).
 template <class E, int kMode>
 int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t stream) {
-  const void* kernel = reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer>);
+  const bool shallow = plan.chains >= kClShallowMinChains;
+  const void* kernel =
+      shallow ? reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsShallow>)
+              : reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep>);
   const int threads = 64 * kClTileWaves;
-  const int resident = cl_resident_blocks(kernel, E::kSlot * 3 + kMode, threads);
+  const int resident = cl_resident_blocks(kernel, (E::kSlot * 3 + kMode) * 2 + (shallow ? 0 : 1),
+                                          threads);
   if (resident <= 0) return -1;
   uint64_t* status = static_cast<uint64_t*>(workspace);
   int64_t ntiles = plan.ntiles;

@@ -120,7 +120,7 @@ SHAPES = [
     (4, 129, 64),     # a last tile of one step (2-byte types)
     (2, 4096, 512),   # 16 chains
     (1, 65536, 64),   # one chain of 512 (1024 in fp32) tiles: the deepest dependency chain
-    (8, 2048, 1024),  # 128 chains, the automatic choice's regime
+    (8, 2048, 1024),  # 128 chains: look-back depth 3 (5 below 128 chains)
 ]
 
 
