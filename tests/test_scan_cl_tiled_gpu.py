@@ -140,12 +140,16 @@ def test_forward_reverse_backward_match_oracle(lib, tiled, dtype, shape):
     check(gg, gg_ref, dtype, f"tiled {shape} grad_gates")
 
 
+# look-back depth 5 (8 chains) and 3 (128 chains)
+DEPTH_SHAPES = [(2, 8192, 256), (8, 1024, 1024)]
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
-def test_exact_on_integer_data(lib, tiled, dtype):
+@pytest.mark.parametrize("shape", DEPTH_SHAPES, ids=str)
+def test_exact_on_integer_data(lib, tiled, dtype, shape):
     """Gates in {0, 1} and small integer tokens: every partial result is exact, whatever the
     composition order, so the tiled kernels must equal the oracle bit for bit."""
     gen = torch.Generator().manual_seed(21)
-    shape = (2, 8192, 256)
     g = (torch.randint(0, 24, shape, generator=gen) > 0).to(dtype)
     x = torch.randint(-3, 4, shape, generator=gen).to(dtype)
     go = torch.randint(-2, 3, shape, generator=gen).to(dtype)
@@ -166,11 +170,12 @@ def test_exact_on_integer_data(lib, tiled, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
-def test_deterministic_and_reverse_is_mirrored_forward(lib, tiled, dtype):
+@pytest.mark.parametrize("batch", [2, 8], ids=["32-chains", "128-chains"])
+def test_deterministic_and_reverse_is_mirrored_forward(lib, tiled, dtype, batch):
     """The carry into a tile is composed the same way on every run, so repeated calls agree
     bit for bit, and reverse(g, x) == flip(forward(flip(g), flip(x))) bit for bit (the tiles
-    of the reverse pass are the mirrored tiles of the forward pass)."""
-    g, x = cl_inputs(8, 4000, 1024, dtype, seed=3)
+    of the reverse pass are the mirrored tiles of the forward pass). Both look-back depths."""
+    g, x = cl_inputs(batch, 4000, 1024, dtype, seed=3)
     gd, xd = g.to(DEVICE), x.to(DEVICE)
     first = abi_fwd(lib, gd, xd, False, ws_check=False)
     for _ in range(3):
