@@ -266,7 +266,8 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 // Look-back: the predecessors of tile k are the earlier tiles of its chain, k-1, k-2, ...
 // The carry into k is always composed the same way, so results do not depend on timing:
 //     carry(k) = agg(k-1) o ... o agg(k-K) applied to y_end(k-K-1)
-// (fewer maps and the zero state near the chain start; K = 3 or 5, fixed by the shape).
+// (fewer maps and the zero state near the chain start; K = 3 or 5, fixed by the shape, the
+// type and the direction).
 // Tiles are claimed in order (Claims over chain groups: within a group all chains' tile 0,
 // then all chains' tile 1, ...), so a tile's predecessors were claimed before it. An
 // aggregate is published by a reduce, which never waits; y_end(k-K-1) by a finish, which
@@ -287,16 +288,17 @@ constexpr int kClTileWaves = 16;
 constexpr int kClTileCols = 64;  // columns per chain and tile
 constexpr int kClDefer = 1;      // steps between a tile's reduce and its finish
 // Aggregates composed onto a predecessor's end value (the look-back depth K, a template
-// parameter of the kernel): 3 with at least kClShallowMinChains chains, where about 2 tiles of
-// a chain are in flight and end(k-4) is almost always published; 5 with fewer chains, where
-// many tiles of a chain are in flight and a finish would otherwise wait for end(k-4) within
-// the same step. Measured on MI355X (bf16 fwd / bwd, us): (2, 65536, 1024), 32 chains,
-// 210 / 276 with 3 against 197 / 270 with 5; fp32 (4, 65536, 1024), 64 chains, 579 / 909
-// against 550 / 909; (8, 65536, 1024), 128 chains, 600 / 937 against 612 / 918. 7 spills
-// registers in the half-type backward.
+// parameter of the kernel): 5 where many tiles of a chain are in flight and a finish would
+// otherwise wait for end(k-4) within the same step, 3 for forward and reverse scans with many
+// chains (about 2 tiles of a chain in flight), where the two extra words cost more than the
+// waits they save. Measured on MI355X, forward with 3 against 5 (us, one box): bf16 64
+// chains 323 / 320, 96 chains 448 / 465, 128 chains 591 / 614; fp32 192 chains 1644 / 1592,
+// 256 chains 271 / 277. The backward measured 0-2 % faster with 5 at every chain count up to
+// 256. 7 spills registers in the half-type backward.
 constexpr int kClAggsShallow = 3;
 constexpr int kClAggsDeep = 5;
-constexpr int64_t kClShallowMinChains = 128;
+constexpr int64_t kClShallowMinChainsHalf = 96;   // forward / reverse, 2-byte types
+constexpr int64_t kClShallowMinChainsF32 = 256;  // forward / reverse, fp32
 static_assert(kClTileWaves * 4 == kClTileCols, "wave w scans the totals of columns 4w..4w+3");
 
 constexpr uint32_t kEndNotPublished = ~0u;
@@ -837,7 +839,9 @@ int cl_resident_blocks(const void* kernel, int slot, int threads) {
 // fails (the caller then takes another path).
 template <class E, int kMode>
 int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t stream) {
-  const bool shallow = plan.chains >= kClShallowMinChains;
+  const bool shallow =
+      kMode != kBwd &&
+      plan.chains >= (E::kSize == 4 ? kClShallowMinChainsF32 : kClShallowMinChainsHalf);
   const void* kernel =
       shallow ? reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsShallow>)
               : reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep>);

@@ -120,7 +120,7 @@ SHAPES = [
     (4, 129, 64),     # a last tile of one step (2-byte types)
     (2, 4096, 512),   # 16 chains
     (1, 65536, 64),   # one chain of 512 (1024 in fp32) tiles: the deepest dependency chain
-    (8, 2048, 1024),  # 128 chains: look-back depth 3 (5 below 128 chains)
+    (8, 2048, 1024),  # 128 chains (look-back depth 3 in the 2-byte forward, else 5)
 ]
 
 
@@ -140,8 +140,9 @@ def test_forward_reverse_backward_match_oracle(lib, tiled, dtype, shape):
     check(gg, gg_ref, dtype, f"tiled {shape} grad_gates")
 
 
-# look-back depth 5 (8 chains) and 3 (128 chains)
-DEPTH_SHAPES = [(2, 8192, 256), (8, 1024, 1024)]
+# look-back depths: 8 chains take 5 everywhere; 128 chains 3 in the 2-byte forward and
+# reverse, 5 otherwise; 256 chains 3 in every forward and reverse; the backward always 5
+DEPTH_SHAPES = [(2, 8192, 256), (8, 1024, 1024), (16, 512, 1024)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
