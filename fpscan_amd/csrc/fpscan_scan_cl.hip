@@ -773,8 +773,8 @@ int launch_cl(const ClArgs& a, hipStream_t stream) {
 }
 
 // Tiled path. It replaces the segments wherever one pass per strip lacks waves, whatever the
-// number of chains, with a persistent grid of every workgroup that fits on the device (at most
-// one per tile). Measured on MI355X, bf16 forward / backward, against the segments: (4, 65536,
+// number of chains, and the one pass from kClTiledMinBytes per tensor, with a persistent grid
+// of every workgroup that fits on the device (at most one per tile). Measured on MI355X, bf16 forward / backward, against the segments: (4, 65536,
 // 1024) 64 chains 341 / 478 us against 484 / 689; (1, 65536, 1024) 16 chains 128 / 166 against
 // 248 / 299; (1, 65536, 64) one chain 112 / 111 against 292 / 304. A cap of 2 workgroups per
 // chain cost 40-150 % below 128 chains.
@@ -792,6 +792,14 @@ struct ClTilePlan {
 // 8-byte words of per-tile status: a 64-bit aggregate and a 32-bit end value per column.
 int64_t cl_status_words(int64_t ntiles) { return ntiles * kClTileCols * 3 / 2; }
 
+// From this size per tensor the tiled pass also replaces the one pass per strip. Measured on
+// MI355X, one pass against tiled, fwd / bwd us: fp32 (16, 4096, 8192), 512 strips, 1466 / 2258
+// against 1119 / 1970; fp32 (512, 256, 4096), 8192 strips, 1223 / 2069 against 1066 / 1799;
+// bf16 (256, 1024, 8192) 2689 / 4490 against 2370 / 3580. Smaller problems with few tiles per
+// chain keep the one pass: fp32 (64, 256, 4096) 143 / 249 against 150 / 246, bf16 (64, 256,
+// 4096) 79 / 135 against 102 / 185.
+constexpr int64_t kClTiledMinBytes = 512ll << 20;
+
 ClTilePlan plan_cl_tiles(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_t, int size,
                          int tiling) {
   ClTilePlan t{false, 0, 0, 0, 0, 0};
@@ -806,7 +814,8 @@ ClTilePlan plan_cl_tiles(int64_t batch, int64_t seqlen, int64_t dim, int64_t str
   if ((steps + 2) * stride_t * size > INT32_MAX) return t;
   if (tiling == 0) {
     const int64_t strips = (dim + 64 * cl_vec(size) - 1) / (64 * cl_vec(size));
-    if (batch * strips >= kClMinTasks || t.nseg < 2) return t;
+    const bool large = batch * seqlen * dim * size >= kClTiledMinBytes;
+    if ((batch * strips >= kClMinTasks && !large) || t.nseg < 2) return t;
   }
   t.use = true;
   t.bytes = (size_t)words * sizeof(uint64_t);

@@ -104,12 +104,13 @@ size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dt
  * state, fp32 arithmetic), without the transposes. Any seqlen >= 1; dim, stride_t and
  * stride_b multiples of 16/itemsize elements; pointers 16-byte aligned; `out` may alias
  * `tokens` or `gates` exactly. With at least 512 strips of 64 16-byte vectors
- * (batch * dim / (64 * 16/itemsize)) one wave scans each strip in one pass. With fewer, the
- * time axis is tiled and needs fpscan_workspace_bytes_cl() bytes of workspace: a single pass
- * whose tiles (64 columns by 128 steps, 64 in fp32) look back along time (3 N s bytes
- * forward, results independent of timing), or, when seqlen fits one tile or a tile's rows
- * span more than a 2 GiB buffer range, segments (aggregates, carries, then the segments
- * again: 5 N s bytes). Without the workspace the call runs one pass per strip
+ * (batch * dim / (64 * 16/itemsize)) and less than 512 MiB per tensor, one wave scans each
+ * strip in one pass. Otherwise the time axis is tiled and needs fpscan_workspace_bytes_cl()
+ * bytes of workspace: a single pass whose tiles (64 columns by 128 steps, 64 in fp32) look
+ * back along time (3 N s bytes forward, results independent of timing). Where a tile does
+ * not apply (seqlen within one tile, or a tile's rows beyond a 2 GiB buffer range), fewer
+ * than 512 strips take segments (aggregates, carries, then the segments again: 5 N s bytes)
+ * and more take the one pass. Without the workspace the call runs one pass per strip
  * (correct, slower), except that a batch slab of more than about 2 GiB needs the workspace
  * (FPSCAN_ERR_WORKSPACE otherwise). Calls sharing a workspace must not overlap.
  * No reference counterpart: the reference supports (batch, dim, seqlen) only and tells callers
@@ -197,7 +198,8 @@ int fpscan_set_launch_override(int waves_per_row, int ring_depth);
 
 /* Path selection for tests and tuning; process-wide. 0: automatic (rows: tiled for problems
  * of at least 512 MiB per tensor, backward from 256 MiB with rows of 128 KiB or more;
- * channel-last: tiled look-back when one pass per strip lacks strips), 1: no tiled look-back (rows streamed; channel-last one
+ * channel-last: tiled look-back when one pass per strip lacks strips or from 512 MiB per
+ * tensor), 1: no tiled look-back (rows streamed; channel-last one
  * pass or segments), 2: tiled whenever possible (rows with 16..1024 sub-chunks; any
  * channel-last problem whose 130-row tile fits a 2 GiB buffer range). Tiled paths need the
  * workspace. No reference counterpart. */

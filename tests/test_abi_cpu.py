@@ -247,15 +247,21 @@ def _cl_tiled_bytes(batch, seqlen, dim, itemsize):
 
 
 def test_channel_last_workspace_plan(cl_lib):
-    """Automatic choice: one pass when batch x strips (64 16-byte vectors each) reaches 512;
-    below that, the tiled single pass (tiles of 64 columns by 16 x 16/itemsize steps) when
-    seqlen spans more than one tile, else segments of about 1024 steps, more if needed for
-    1024 wave tasks, never below 64 steps, with one (A, B) pair of 8 bytes per segment per
-    column."""
+    """Automatic choice: one pass when batch x strips (64 16-byte vectors each) reaches 512
+    and a tensor is below 512 MiB; otherwise the tiled single pass (tiles of 64 columns by
+    16 x 16/itemsize steps) when seqlen spans more than one tile, else segments of about 1024
+    steps, more if needed for 1024 wave tasks, never below 64 steps, with one (A, B) pair of
+    8 bytes per segment per column (or the one pass, with 512 strips or more)."""
     w = cl_lib.fpscan_workspace_bytes_cl
-    assert w(64, 1024, 8192, 8192, 0, 0) == 0  # 64 x 32 strips: one pass
     assert w(64, 256, 4096, 4096, 0, 0) == 0  # config 5 in channel-last form: 1024 strips
-    assert w(16, 4096, 8192, 8192, 0, 0) == 0  # 512 strips
+    assert w(64, 256, 4096, 4096, 2, 0) == 0  # bf16, 512 strips, 128 MiB: one pass
+    assert w(32, 511, 8192, 8192, 0, 0) == 0  # fp32, 1024 strips, just below 512 MiB
+    # 512 MiB and more per tensor: tiled whatever the strips
+    assert w(32, 512, 8192, 8192, 0, 0) == _cl_tiled_bytes(32, 512, 8192, 4)
+    assert w(64, 1024, 8192, 8192, 0, 0) == _cl_tiled_bytes(64, 1024, 8192, 4)  # 2048 strips
+    assert w(16, 4096, 8192, 8192, 0, 0) == _cl_tiled_bytes(16, 4096, 8192, 4)  # 512 strips
+    # ... unless seqlen fits one tile: fp32 (8192, 64, 1024), 2 GiB, one pass
+    assert w(8192, 64, 1024, 1024, 0, 0) == 0
     assert w(1, 100, 64, 64, 0, 0) == _cl_tiled_bytes(1, 100, 64, 4)  # two 64-step tiles
     # bf16 (8, 65536, 1024): 16 strips, 128 chains -> tiled, 512 tiles of 128 steps per chain
     assert w(8, 65536, 1024, 1024, 2, 0) == _cl_tiled_bytes(8, 65536, 1024, 2) == 50332800
