@@ -273,3 +273,28 @@ def test_padded_strides(lib, tiled, dtype):
     mask.as_strided((B, L, D), (sb, st, 1)).fill_(False)
     for buf in (outb, ggb, gxb):
         assert (buf.cpu()[mask] == -3.0).all(), "padding was written"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_large_problem_with_many_strips_is_tiled(lib, dtype):
+    """The automatic choice from 512 MiB per tensor: tiled even with enough strips for one
+    pass (bf16 (64, 1024, 8192): 1024 strips, 8192 chains, 1 GiB; fp32 (32, 512, 8192): 1024
+    strips, exactly 512 MiB). Checked through the C ABI (workspace of the tiled size, every
+    aggregate published, no overrun), against the oracle on sampled columns, and bit for bit
+    against reverse = flip(forward(flip))."""
+    shape = (64, 1024, 8192) if dtype == torch.bfloat16 else (32, 512, 8192)
+    B, L, D = shape
+    gen = torch.Generator(device=DEVICE).manual_seed(9)
+    g = (0.99 + 0.01 * torch.rand(shape, generator=gen, device=DEVICE)).to(dtype)
+    x = (torch.randn(shape, generator=gen, device=DEVICE) / L).to(dtype)
+    assert lib.fpscan_workspace_bytes_cl(B, L, D, D, _CODE[dtype], 0) == (
+        tile_geometry(B, L, D, dtype)[2] * 768 + _EXTRA_WORDS * 8)
+    out = abi_fwd(lib, g, x, False)
+    rows = torch.linspace(0, B - 1, 4).long()
+    cols = torch.linspace(0, D - 1, 24).long()
+    sel = lambda t: t[rows][:, :, cols].cpu()  # noqa: E731
+    check(sel(out), oracle.scan_f64_channel_last(sel(g), sel(x)), dtype, f"large {shape}")
+    rev = abi_fwd(lib, g, x, True, ws_check=False)
+    mirrored = abi_fwd(lib, g.flip(1).contiguous(), x.flip(1).contiguous(), False,
+                       ws_check=False).flip(1)
+    assert bits_equal(rev, mirrored)
