@@ -3,9 +3,9 @@ with a look-back along seqlen (chains of 64 columns, tiles of 128 steps in 2-byt
 in fp32), against the CPU oracle (oracle.scan_f64_channel_last / scan_bwd_f64_channel_last,
 pinned by tests/test_oracle.py).
 
-fpscan_set_tiling(2) forces the tiled path on every shape here; the automatic choice takes it
-wherever there are too few strips for one pass and more than one tile of steps. Besides the
-oracle: the
+fpscan_set_tiling(2) forces the tiled path on most shapes here; the automatic choice takes it
+wherever there are too few strips for one pass, or a tensor is 512 MiB or more, and seqlen
+spans more than one tile (tested at its real size last). Besides the oracle: the
 workspace after a call (every tile's aggregate published, no wait overrun, claim counters at
 or past their group sizes), bit-exactness on integer data, run-to-run determinism and the
 reverse = flip(forward(flip)) identity bit for bit (the carry into a tile is always composed
