@@ -774,10 +774,11 @@ int launch_cl(const ClArgs& a, hipStream_t stream) {
 
 // Tiled path. It replaces the segments wherever one pass per strip lacks waves, whatever the
 // number of chains, and the one pass from kClTiledMinBytes per tensor, with a persistent grid
-// of every workgroup that fits on the device (at most one per tile). Measured on MI355X, bf16 forward / backward, against the segments: (4, 65536,
-// 1024) 64 chains 341 / 478 us against 484 / 689; (1, 65536, 1024) 16 chains 128 / 166 against
-// 248 / 299; (1, 65536, 64) one chain 112 / 111 against 292 / 304. A cap of 2 workgroups per
-// chain cost 40-150 % below 128 chains.
+// of every workgroup that fits on the device (at most one per tile). Measured on MI355X, bf16
+// forward / backward, against the segments: (4, 65536, 1024) 64 chains 341 / 478 us against
+// 484 / 689; (1, 65536, 1024) 16 chains 128 / 166 against 248 / 299; (1, 65536, 64) one chain
+// 112 / 111 against 292 / 304. A cap of 2 workgroups per chain cost 40-150 % below 128
+// chains.
 
 struct ClTilePlan {
   bool use;
