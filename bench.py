@@ -145,12 +145,14 @@ def cpu_baseline(gates, tokens, grad_out, target_s):
         "sample": f"{rows} of {rows_total} rows x {L} {SHORT[gates.dtype]}: Hillis-Steele "
                   f"forward + composed backward (eval/baselines.py:40-61, fpscan/ops.py:69-83), "
                   f"p50 of 3 runs ({p50:.2f} s each)",
-        "cpu_model": platform.processor() or _cpu_model(),
+        "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
     }
 
 
 def _cpu_model():
+    """The host CPU's model string from /proc/cpuinfo (platform.processor() only says
+    'x86_64' on Linux)."""
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -158,7 +160,38 @@ def _cpu_model():
                     return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return "unknown"
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline_c1(warmup=3, iters=20):
+    """BASELINE config 1 on the host cores: the reference's CPU path (Hillis-Steele
+    ``parallel_scan_torch`` forward, eval/baselines.py:40-61) on fp32 B2 D256 L1024 with the
+    reference test's distributions, warmup 3 then p50 of 20 (GB/s at 3*N*4 bytes)."""
+    import oracle  # the cpu_baseline leg
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    B, D, L = WORKLOADS["c1"][:3]
+    gen = torch.Generator().manual_seed(0)
+    g = 0.99 + 0.01 * torch.rand(B, D, L, generator=gen)
+    x = torch.randn(B, D, L, generator=gen) / L
+    for _ in range(warmup):
+        oracle.parallel_scan_torch(g, x)
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        oracle.parallel_scan_torch(g, x)
+        times.append(time.perf_counter() - t0)
+    p50 = statistics.median(times)
+    return {
+        "value": round(3 * B * D * L * 4 / p50 / 1e9, 4),
+        "unit": "GB/s",
+        "p50_ms": round(p50 * 1e3, 4),
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"config 1: fp32 B{B} D{D} L{L} Hillis-Steele forward (eval/baselines.py:40-61),"
+                  f" warmup {warmup}, p50 of {iters}",
+        "cpu_model": _cpu_model(),
+    }
 
 
 def load_traffic(workload, dtype_short):
@@ -175,11 +208,12 @@ def load_traffic(workload, dtype_short):
 
 
 # ------------------------------------------------------------------------------ workloads
-def bench_headline(args):
+def measure_training_step(B, D, L, dtype, dist, steps, warmup, workload):
+    """One dtype of the headline workload: K bracketed fwd+bwd steps, their per-step p50/p90,
+    and each kernel timed alone (HIP events on the stream the kernels run on). Returns the
+    figures and the inputs (for the CPU baseline)."""
     import fpscan_amd
 
-    B, D, L, dname, dist = WORKLOADS[args.workload]
-    dtype = DTYPES[args.dtype or dname]
     N = B * D * L
     s = torch.empty((), dtype=dtype).element_size()
     gates, tokens, grad_out = make_inputs(B, D, L, dtype, dist, seed=0)
@@ -190,58 +224,42 @@ def bench_headline(args):
         out = fpscan_amd.pscan(g, x)
         return torch.autograd.grad(out, (g, x), grad_out)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     # K timed steps, bracketed by a synchronisation on both sides (one process, one GPU)
     start, end = _events(2)
     t0 = time.perf_counter()
     start.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     end.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    total_ms = start.elapsed_time(end)
-    ms_per_step = total_ms / args.steps
-    step_p = time_each(step, 1, args.steps)
+    ms_per_step = start.elapsed_time(end) / steps
+    step_p = time_each(step, 1, steps)
+    del g, x
 
     # kernels alone
     out = torch.empty_like(tokens)
     gg = torch.empty_like(gates)
     gx = torch.empty_like(gates)
-    fwd_t = time_each(lambda: fpscan_amd.scan_forward(gates, tokens, out=out), 2, args.steps)
+    fwd_t = time_each(lambda: fpscan_amd.scan_forward(gates, tokens, out=out), 2, steps)
     y = fpscan_amd.scan_forward(gates, tokens)
-    bwd_t = time_each(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx), 2,
-                      args.steps)
+    bwd_t = time_each(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx), 2, steps)
+    del out, gg, gx, y
     fwd_avg, bwd_avg = statistics.mean(fwd_t), statistics.mean(bwd_t)
     bwd_bytes = 5 * N * s
     achieved = bwd_bytes / (bwd_avg / 1e3) / 1e9
-    traffic, traffic_src = load_traffic(args.workload, SHORT[dtype])
+    traffic, traffic_src = load_traffic(workload, SHORT[dtype])
     value = 8 * N * s / (ms_per_step / 1e3) / 1e9
     dcode = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
     tiled = fpscan_amd.ops._load_extension().workspace_bytes(B, D, L, dcode, 1) > 0
     bwd_kernel = ("scan_tiles<bwd> (fused backward, persistent tiles with look-back)" if tiled
                   else "scan_long_rows<bwd> (fused backward, one block per row)")
-
     res = {
-        "metric": METRIC,
         "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": SHORT[dtype],
-        "data": "synthetic",
-        "config": {
-            "workload": f"{args.workload}: pscan fwd+bwd B{B} D{D} L{L} {SHORT[dtype]}",
-            "batch": B, "dim": D, "seqlen": L, "inputs": dist,
-            "parallelism": "none (1 GPU; rows independent)",
-        },
         "p50_ms": round(percentile(step_p, 0.5), 5),
         "p90_ms": round(percentile(step_p, 0.9), 5),
         "hbm_frac": round(value / HBM_PEAK_GBPS, 4),
@@ -261,12 +279,52 @@ def bench_headline(args):
             "traffic_source": traffic_src,
         },
         "wall_ms_timed_region": round(wall_ms, 3),
-        "device": torch.cuda.get_device_name(),
     }
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(gates, tokens, grad_out, args.cpu_seconds)
-    else:
+    return res, (gates, tokens, grad_out)
+
+
+def bench_headline(args):
+    B, D, L, dname, dist = WORKLOADS[args.workload]
+    dtype = DTYPES[args.dtype or dname]
+    main, inputs = measure_training_step(B, D, L, dtype, dist, args.steps, args.warmup,
+                                         args.workload)
+    res = {
+        "metric": METRIC,
+        "value": main.pop("value"),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": SHORT[dtype],
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: pscan fwd+bwd B{B} D{D} L{L} {SHORT[dtype]}",
+            "batch": B, "dim": D, "seqlen": L, "inputs": dist,
+            "parallelism": "none (1 GPU; rows independent)",
+        },
+    }
+    res.update(main)
+    res["device"] = torch.cuda.get_device_name()
+    if args.no_cpu_baseline:
         res["cpu_baseline"] = None
+    else:
+        res["cpu_baseline"] = cpu_baseline(*inputs, args.cpu_seconds)
+    del inputs
+    torch.cuda.empty_cache()
+    if args.workload == "c4" and dtype != torch.float32 and not args.no_fp32:
+        # the north star's second dtype, fp32 (the reference's only published dtype): the same
+        # step at the same shape, reported beside the headline line's bf16 figures
+        f32, _ = measure_training_step(B, D, L, torch.float32, dist, args.steps, args.warmup,
+                                       args.workload)
+        f32["config"] = f"{args.workload}: pscan fwd+bwd B{B} D{D} L{L} f32"
+        res["fp32"] = f32
+        torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        res["cpu_baseline_c1"] = cpu_baseline_c1()
     return res
 
 
@@ -442,6 +500,8 @@ def main():
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fp32", action="store_true",
+                    help="c4: skip the fp32 step reported beside the bf16 headline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--launch", default=None, help="waves_per_row,ring_depth override")
     ap.add_argument("--calibrate-copy", action="store_true",

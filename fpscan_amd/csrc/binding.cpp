@@ -18,6 +18,8 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <hip/hip_runtime_api.h>
+
 #include <string>
 #include <utility>
 
@@ -70,6 +72,22 @@ void check_status(int status) {
               ")");
 }
 
+// The stream a call is about to launch on, refused while it captures a HIP graph: the one
+// capture of these kernels through torch.cuda.graph that was run (the streaming forward and
+// backward) ended in a host segmentation fault inside capture_end, with a cause not found, so
+// a capture fails here with an error instead. Eager launches on any stream are unaffected.
+void* launch_stream(const at::Tensor& like) {
+  hipStream_t stream =
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(like.device().index()).stream();
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  const bool capturing = hipStreamIsCapturing(stream, &capture) == hipSuccess &&
+                         capture != hipStreamCaptureStatusNone;
+  TORCH_CHECK(!capturing, "fpscan: HIP graph capture of the fpscan kernels through the torch "
+              "binding is not supported by this build (a captured run crashed the host in "
+              "graph instantiation); call it outside the captured region");
+  return stream;
+}
+
 at::Tensor fullscan_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tensor& out,
                             bool reverse) {
   check_input(Ax, "Ax");
@@ -81,7 +99,7 @@ at::Tensor fullscan_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at
   if (Bx.numel() == 0) return out;
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
-  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(Bx.device().index()).stream();
+  void* stream = launch_stream(Bx);
   // contiguous (batch, dim, seqlen): the packed strides (torch may report any stride for a
   // size-1 dimension of a contiguous tensor)
   const int64_t L = Bx.size(2), D = Bx.size(1);
@@ -123,8 +141,7 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward(const at::Tensor& gates,
               "grad_gates and grad_tokens must be distinct");
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(gates.device());
-  void* stream =
-      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(gates.device().index()).stream();
+  void* stream = launch_stream(gates);
   const int dt = dtype_code(gates.scalar_type());
   const size_t ws_bytes =
       fpscan_workspace_bytes(gates.size(0), gates.size(1), gates.size(2), dt, FPSCAN_OP_BWD);
@@ -163,7 +180,7 @@ at::Tensor fullscan_forward_cl(const at::Tensor& Ax, const at::Tensor& Bx, const
   if (Bx.numel() == 0) return out;
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
-  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(Bx.device().index()).stream();
+  void* stream = launch_stream(Bx);
   const int64_t B = Bx.size(0), L = Bx.size(1), D = Bx.size(2);
   const int dt = dtype_code(Bx.scalar_type());
   const size_t ws_bytes = fpscan_workspace_bytes_cl(B, L, D, D, dt, FPSCAN_OP_FWD);
@@ -201,8 +218,7 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward_cl(const at::Tensor& gates,
               "grad_gates and grad_tokens must be distinct");
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(gates.device());
-  void* stream =
-      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(gates.device().index()).stream();
+  void* stream = launch_stream(gates);
   const int64_t B = gates.size(0), L = gates.size(1), D = gates.size(2);
   const int dt = dtype_code(gates.scalar_type());
   const size_t ws_bytes = fpscan_workspace_bytes_cl(B, L, D, D, dt, FPSCAN_OP_BWD);
@@ -247,7 +263,7 @@ void dimwise_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tenso
   if (Bx.numel() == 0) return;
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
-  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(Bx.device().index()).stream();
+  void* stream = launch_stream(Bx);
   const int status = fpscan_dimwise_fwd(Ax.data_ptr(), Bx.data_ptr(), Bh.data_ptr(),
                                         Wq.data_ptr(), Wk.data_ptr(), B, D, L,
                                         dtype_code(Bx.scalar_type()), stream);
@@ -276,8 +292,7 @@ at::Tensor fullscan_forward_softplus(const at::Tensor& z, const at::Tensor& rate
   check_seqlen(tokens.size(2));
   if (tokens.numel() == 0) return out;
   c10::hip::HIPGuardMasqueradingAsCUDA guard(tokens.device());
-  void* stream =
-      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(tokens.device().index()).stream();
+  void* stream = launch_stream(tokens);
   const int64_t D = tokens.size(1), L = tokens.size(2);
   const int status = fpscan_scan_fwd_softplus(
       z.data_ptr(), rate.data_ptr<float>(), tokens.data_ptr(), out.data_ptr(), tokens.size(0),
@@ -317,13 +332,22 @@ void fullscan_backward_softplus(const at::Tensor& z, const at::Tensor& rate,
   TORCH_CHECK(grad_z.data_ptr() != grad_tokens.data_ptr(),
               "grad_z and grad_tokens must be distinct");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(z.device());
-  void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(z.device().index()).stream();
+  void* stream = launch_stream(z);
   const int64_t D = z.size(1), L = z.size(2);
   const int status = fpscan_scan_bwd_softplus(
       z.data_ptr(), rate.data_ptr<float>(), out.data_ptr(), grad_out.data_ptr(),
       grad_z.data_ptr(), grad_tokens.data_ptr(), grad_rate_rows.data_ptr<float>(), z.size(0), D,
       L, D * L, L, dtype_code(z.scalar_type()), stream);
   check_status(status);
+}
+
+// Look-back waits that gave up on the tensors' device since the library was loaded (waits for
+// the device first).
+uint64_t lookback_overruns(int64_t device) {
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(at::Device(at::kCUDA, (c10::DeviceIndex)device));
+  unsigned long long n = 0;
+  check_status(fpscan_lookback_overruns(&n));
+  return n;
 }
 
 int set_launch_override(int waves_per_row, int ring_depth) {
@@ -369,6 +393,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "tuning hook: force waves per row / ring depth (0 = built-in choice)",
         pybind11::arg("waves_per_row"), pybind11::arg("ring_depth"));
   m.def("abi_version", []() { return fpscan_abi_version(); });
+  m.def("lookback_overruns", &lookback_overruns,
+        "look-back waits of the tiled kernels that gave up on this device (0 in a correct run)",
+        pybind11::arg("device"));
+  m.def("set_lookback_test_hook", [](int64_t unpublished_tile, int spin_limit) {
+    TORCH_CHECK(fpscan_set_lookback_test_hook(unpublished_tile, spin_limit) == FPSCAN_OK,
+                "spin_limit must be >= 0");
+  }, "test hook: never publish one tile's map and give up waits after spin_limit polls "
+     "(-1, 0 restore the defaults)", pybind11::arg("unpublished_tile"),
+        pybind11::arg("spin_limit"));
   m.def("set_tiling", [](int mode) {
     TORCH_CHECK(fpscan_set_tiling(mode) == FPSCAN_OK, "tiling mode must be 0, 1 or 2");
   }, "path selection: 0 automatic, 1 no tiled look-back (rows streamed; channel-last one pass "

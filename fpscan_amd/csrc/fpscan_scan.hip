@@ -60,7 +60,15 @@ struct Args {
   // partial sum of d loss / d rate per row (rows floats, may be null)
   const float* rate;
   float* grad_rate_rows;
+  // tiled path: polls before a look-back wait gives up, and a tile whose map is never
+  // published (-1: none; a test hook that forces a wait to give up)
+  int64_t skip_publish;
+  int32_t spin_limit;
 };
+
+// Look-back waits that gave up on this device since the library was loaded (the tiled row
+// kernel's; the channel-last kernels keep their own). Read by fpscan_lookback_overruns.
+static __device__ unsigned long long g_row_overruns;
 
 
 __device__ __forceinline__ int64_t row_offset(const Args& a, int64_t row) {
@@ -452,8 +460,10 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
 // workgroup that is already running, and a tile's predecessors were claimed before it. So,
 // within each claim group, the workgroup owning the lowest unpublished tile is running and
 // only ever waits on lower tiles, which are published; it makes progress. Each wait is also
-// bounded; a wait that exceeds the bound (which a correct launch never reaches) bumps the
-// overrun word after the status array and proceeds, so the kernel always terminates.
+// bounded; a wait that exceeds the bound (which a correct launch never reaches) counts itself
+// in the overrun word after the status array and in a per-device counter that the host can
+// read, replaces the missing maps by NaN maps, so that the tile's outputs are NaN rather than
+// plausible, and proceeds, so the kernel always terminates.
 //
 // Workspace layout (8-byte words): [0, ntiles) tile status, [ntiles] wait overruns,
 // [ntiles + kCounterStride * (1 + g)] claim counter of group g.
@@ -626,7 +636,7 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
       if constexpr (TW > 8) combine_from_row<8>(eA, eB);
       const float cur_pA = (w > 0) ? readlane(eA, w - 1) : 1.0f;
       const float cur_pB = (w > 0) ? readlane(eB, w - 1) : 0.0f;
-      const bool publisher = cur_live && w == 0 && lane == 0;
+      const bool publisher = cur_live && w == 0 && lane == 0 && cur.tile != a.skip_publish;
       status_store(st, publisher ? (uint32_t)(cur.tile * sizeof(uint64_t)) : kNoOffset,
                    pack_map(readlane(eA, TW - 1), readlane(eB, TW - 1)));
 
@@ -644,11 +654,16 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
           word = in_row ? __hip_atomic_load(status + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                         : 0ull;
           if (__builtin_amdgcn_ballot_w64(word == kNotPublished) == 0) break;
-          if (it == kSpinLimit) {
-            if (lane == 0)
+          if (it >= a.spin_limit) {
+            // only after an overrun: count it where the caller can see it, and make the
+            // tile's outputs NaN (a NaN map poisons the composed carry) instead of plausible
+            if (lane == 0) {
               __hip_atomic_fetch_add(status + ntiles, 1ull, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
-            word = 0;  // only after an overrun: keep the result finite
+              __hip_atomic_fetch_add(&g_row_overruns, 1ull, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+            }
+            word = word == kNotPublished ? kPoisonMap : word;
             break;
           }
         }
@@ -780,9 +795,13 @@ __global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
 // ---------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------
+// Process-wide tuning and test hooks (fpscan_set_launch_override, fpscan_set_tiling,
+// fpscan_set_lookback_test_hook); every setting computes the same recurrence.
 std::atomic<int> g_override_w{0};
 std::atomic<int> g_override_u{0};
 std::atomic<int> g_tiling{0};  // 0 automatic, 1 row streaming only, 2 tiled when possible
+std::atomic<int64_t> g_hook_skip_publish{-1};
+std::atomic<int> g_hook_spin_limit{0};  // 0: kSpinLimit
 
 // Tiled path geometry: TW sub-chunks per tile, at most 64 tiles per row (one look-back window)
 constexpr int kTileWaves = 16;
@@ -925,6 +944,9 @@ int run_tiled(const Args& a, const TilePlan& plan, void* workspace, hipStream_t 
     return FPSCAN_ERR_LAUNCH;
   const int64_t grid = plan.ntiles < resident ? plan.ntiles : resident;
   Args copy = a;
+  copy.skip_publish = g_hook_skip_publish.load(std::memory_order_relaxed);
+  const int spin = g_hook_spin_limit.load(std::memory_order_relaxed);
+  copy.spin_limit = spin > 0 ? spin : kSpinLimit;
   int tpr_log2 = 0;
   while ((1 << tpr_log2) < plan.tpr) ++tpr_log2;
   void* kargs[] = {&copy, &status, &tpr_log2, &ntiles};
@@ -1017,9 +1039,28 @@ int validate(int64_t batch, int64_t dim, int64_t seqlen, int64_t stride_b, int64
 
 }  // namespace
 
-// Path selection set by fpscan_set_tiling, read by the channel-last launcher as well.
+// Path selection set by fpscan_set_tiling and the look-back test hook, read by the
+// channel-last launcher as well; the channel-last counter of given-up waits.
 namespace fpscan_detail {
 int tiling_mode() { return g_tiling.load(std::memory_order_relaxed); }
+int64_t hook_skip_publish() { return g_hook_skip_publish.load(std::memory_order_relaxed); }
+int hook_spin_limit() {
+  const int spin = g_hook_spin_limit.load(std::memory_order_relaxed);
+  return spin > 0 ? spin : kSpinLimit;
+}
+int cl_overruns(unsigned long long* count);  // fpscan_scan_cl.hip
+}  // namespace fpscan_detail
+
+namespace fpscan_detail {
+// The row kernel's counter of given-up waits on the current device (a synchronous copy).
+int row_overruns(unsigned long long* count) {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_row_overruns)) != hipSuccess || p == nullptr)
+    return FPSCAN_ERR_DEVICE;
+  if (hipMemcpy(count, p, sizeof(*count), hipMemcpyDeviceToHost) != hipSuccess)
+    return FPSCAN_ERR_DEVICE;
+  return FPSCAN_OK;
+}
 }  // namespace fpscan_detail
 
 extern "C" {
@@ -1128,6 +1169,26 @@ const char* fpscan_strerror(int status) {
     case FPSCAN_ERR_DEVICE: return "could not query the current HIP device";
     default: return "unknown fpscan status";
   }
+}
+
+int fpscan_lookback_overruns(unsigned long long* count) {
+  if (count == nullptr) return FPSCAN_ERR_NULL;
+  if (hipDeviceSynchronize() != hipSuccess) return FPSCAN_ERR_DEVICE;
+  unsigned long long rows = 0, cl = 0;
+  int st = fpscan_detail::row_overruns(&rows);
+  if (st != FPSCAN_OK) return st;
+  st = fpscan_detail::cl_overruns(&cl);
+  if (st != FPSCAN_OK) return st;
+  *count = rows + cl;
+  return FPSCAN_OK;
+}
+
+int fpscan_set_lookback_test_hook(int64_t unpublished_tile, int spin_limit) {
+  if (spin_limit < 0) return FPSCAN_ERR_SHAPE;
+  g_hook_skip_publish.store(unpublished_tile < 0 ? -1 : unpublished_tile,
+                            std::memory_order_relaxed);
+  g_hook_spin_limit.store(spin_limit, std::memory_order_relaxed);
+  return FPSCAN_OK;
 }
 
 int fpscan_abi_version(void) { return FPSCAN_ABI_VERSION; }

@@ -32,6 +32,8 @@
 
 namespace fpscan_detail {
 int tiling_mode();  // fpscan_set_tiling's setting (fpscan_scan.hip)
+int64_t hook_skip_publish();  // fpscan_set_lookback_test_hook's settings (fpscan_scan.hip)
+int hook_spin_limit();
 }  // namespace fpscan_detail
 
 namespace {
@@ -62,7 +64,15 @@ struct ClArgs {
   int32_t strips;    // per batch: ceil(dim / (64 V))
   int64_t chains;    // tiled path: batch * strips64
   int64_t strips64;  // tiled path, per batch: ceil(dim / 64)
+  // tiled path: a tile whose aggregates are never published (-1: none; a test hook that
+  // forces waits to give up) and the polls before a wait gives up
+  int64_t skip_publish;
+  int32_t spin_limit;
 };
+
+// Look-back waits of the tiled channel-last kernel that gave up on this device since the
+// library was loaded. Read by fpscan_lookback_overruns.
+static __device__ unsigned long long g_cl_overruns;
 
 // Loaded operands of one time step for one lane.
 template <int kMode>
@@ -553,7 +563,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
         combine_from_row<8>(eA, eB);
         if (i < 15) pref[i + 1][col] = f32x2{eA, eB};
         if (i == 15) aggs[u][col] = f32x2{eA, eB};
-        const bool publish = cur_live && i == 15;
+        const bool publish = cur_live && i == 15 && cur.tile != a.skip_publish;
         status_store(st,
                      publish ? (uint32_t)((cur.tile * kClTileCols + col) * sizeof(uint64_t))
                              : kNoOffset,
@@ -574,7 +584,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
           // give up at once, so that the launch still ends soon)
           const bool overran = __hip_atomic_load(status + nstatus, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT) != 0;
-          for (int it = overran ? kSpinLimit : 0;; ++it) {
+          for (int it = overran ? a.spin_limit : 0;; ++it) {
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
             for (int j = 0; j < K; ++j) {
@@ -591,17 +601,22 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
             if (__builtin_amdgcn_ballot_w64(agg_missing(held_agg, na) ||
                                             (fin.seg > K && held_end == kEndNotPublished)) == 0)
               break;
-            if (it == kSpinLimit) {
-              if (lane == 0)
+            if (it >= a.spin_limit) {
+              if (lane == 0) {
                 __hip_atomic_fetch_add(status + nstatus, 1ull, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-              break;  // only after an overrun: the words still missing count as zeros
+                __hip_atomic_fetch_add(&g_cl_overruns, 1ull, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+              }
+              break;
             }
           }
+          // only after an overrun: the words still missing become NaN, so that this tile's
+          // outputs, its end values and every carry composed from them are NaN, not plausible
 #pragma unroll
           for (int j = 0; j < K; ++j)
-            held_agg[j] = held_agg[j] == kNotPublished ? 0ull : held_agg[j];
-          held_end = held_end == kEndNotPublished ? 0u : held_end;
+            held_agg[j] = held_agg[j] == kNotPublished ? kPoisonMap : held_agg[j];
+          held_end = held_end == kEndNotPublished ? kPoisonValue : held_end;
         }
         // carry = agg(k-1) o ... o agg(k-na) applied to y_end(k-na-1), or to the zero state
         float carry = fin.seg > K ? __uint_as_float(held_end) : 0.0f;
@@ -875,6 +890,8 @@ int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t 
   a.nseg = (int32_t)plan.nseg;
   a.seg_len = cl_tile_steps<E>();
   a.ws = nullptr;
+  a.skip_publish = fpscan_detail::hook_skip_publish();
+  a.spin_limit = fpscan_detail::hook_spin_limit();
   void* kargs[] = {&a, &status, &ntiles};
   const hipError_t err =
       hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), kargs, 0, stream);
@@ -964,6 +981,18 @@ int validate_cl(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_b, in
 }
 
 }  // namespace
+
+namespace fpscan_detail {
+// The channel-last counter of given-up waits on the current device (a synchronous copy).
+int cl_overruns(unsigned long long* count) {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_cl_overruns)) != hipSuccess || p == nullptr)
+    return FPSCAN_ERR_DEVICE;
+  if (hipMemcpy(count, p, sizeof(*count), hipMemcpyDeviceToHost) != hipSuccess)
+    return FPSCAN_ERR_DEVICE;
+  return FPSCAN_OK;
+}
+}  // namespace fpscan_detail
 
 extern "C" {
 

@@ -369,7 +369,11 @@ __device__ __forceinline__ void segment_scan_k(float (&A)[K], float (&B)[K], int
 // counter of group g.
 // ---------------------------------------------------------------------------------------
 constexpr uint64_t kNotPublished = ~0ull;
-constexpr int kSpinLimit = 1 << 16;  // polls of ~1 us each (a device-coherent load)
+// The map (NaN, NaN): stands in for a predecessor whose wait gave up, so that everything
+// composed from it is NaN.
+constexpr uint64_t kPoisonMap = 0x7fc000007fc00000ull;
+constexpr uint32_t kPoisonValue = 0x7fc00000u;
+constexpr int kSpinLimit = 1 << 16;  // default polls of ~1 us each (a device-coherent load)
 
 __device__ __forceinline__ uint32_t canonical_bits(float v) {
   return v != v ? 0x7fc00000u : __float_as_uint(v);

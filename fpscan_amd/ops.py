@@ -255,6 +255,31 @@ def set_launch_override(waves_per_row: int = 0, ring_depth: int = 0) -> None:
     _load_extension().set_launch_override(int(waves_per_row), int(ring_depth))
 
 
+def lookback_overruns(device=None) -> int:
+    """Look-back waits of the tiled kernels that gave up on ``device`` (default: the current
+    one) since the library was loaded; 0 in a correct run. Waits for the device first. A wait
+    gives up only if an earlier tile stalls for tens of milliseconds; the affected outputs
+    are then NaN, and this count says so."""
+    dev = torch.cuda.current_device() if device is None else torch.device(device).index
+    return int(_load_extension().lookback_overruns(int(dev if dev is not None else 0)))
+
+
+def check_lookback(device=None) -> None:
+    """Raises RuntimeError if any look-back wait has given up on ``device`` (whose outputs
+    then hold NaN); a cheap end-of-step check for long runs."""
+    n = lookback_overruns(device)
+    if n:
+        raise RuntimeError(f"fpscan: {n} look-back wait(s) of the tiled scan gave up on this "
+                           "device; the outputs of the affected tiles are NaN")
+
+
+def set_lookback_test_hook(unpublished_tile: int = -1, spin_limit: int = 0) -> None:
+    """Test hook (process-wide): the tiled kernels never publish tile ``unpublished_tile``'s
+    map, and a look-back wait gives up after ``spin_limit`` polls (0: the default). The
+    defaults restore normal operation."""
+    _load_extension().set_lookback_test_hook(int(unpublished_tile), int(spin_limit))
+
+
 def set_tiling(mode: int = 0) -> None:
     """Path selection (process-wide) for long rows and channel-last scans: 0 automatic,
     1 no tiled look-back (rows streamed; channel-last one pass per strip or segments),

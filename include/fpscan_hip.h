@@ -11,10 +11,22 @@
  * Element types: fp32, fp16 and bf16; all arithmetic is fp32, outputs are rounded to
  * nearest-even once. seqlen must be a power of two in [32, 65536], as in the reference.
  *
- * All entry points are asynchronous on `stream` (a hipStream_t; NULL = the null stream),
- * allocate nothing, keep no state between calls and are safe to call from several host
- * threads. Pointers are device pointers on the current HIP device; they must be 16-byte
- * aligned and the strides must be multiples of 16 bytes (16/itemsize elements).
+ * All scan entry points are asynchronous on `stream` (a hipStream_t; NULL = the null
+ * stream), allocate nothing and are safe to call from several host threads. Pointers are
+ * device pointers on the current HIP device; they must be 16-byte aligned and the strides
+ * must be multiples of 16 bytes (16/itemsize elements).
+ *
+ * State the library keeps: (1) process-wide tuning and test hooks -- fpscan_set_tiling,
+ * fpscan_set_launch_override, fpscan_set_lookback_test_hook -- which change the path taken
+ * (and so fpscan_workspace_bytes' answer and the fp32 rounding order), never the recurrence;
+ * they are meant for tests and tuning sweeps and are not synchronised with calls in flight;
+ * (2) per device: a count of look-back waits that gave up (fpscan_lookback_overruns).
+ *
+ * Look-back waits: the tiled paths chain tiles through status words and each wait for an
+ * earlier tile is bounded. A wait that gives up -- which a correct launch never does, but a
+ * predecessor stalled for tens of milliseconds (preemption, another process) could cause --
+ * makes its tile's outputs, and everything computed from them, NaN instead of plausible
+ * values, and counts itself in a per-device counter that fpscan_lookback_overruns reads.
  *
  * Workspace: large problems run fastest on the tiled path, which needs
  * fpscan_workspace_bytes() bytes of device memory (one 8-byte word per tile plus 1152 bytes
@@ -188,15 +200,28 @@ const char* fpscan_strerror(int status);
 /* FPSCAN_ABI_VERSION of the loaded library. */
 int fpscan_abi_version(void);
 
-/* Launch-shape override for tuning sweeps; process-wide, not synchronised with calls in
- * flight on other threads. waves_per_row in {0,1,2,4,8,16}, ring_depth in 0..4;
+/* Look-back waits (row and channel-last tiled kernels) that gave up on the current device
+ * since the library was loaded; 0 in a correct run. Waits for all work on the device first
+ * (hipDeviceSynchronize), then copies the device counters. No reference counterpart: the
+ * reference keeps every carry inside one block (full_scan.cu:77-175) and has no such wait. */
+int fpscan_lookback_overruns(unsigned long long* count);
+
+/* Test hook, process-wide: the tiled kernels never publish the map(s) of tile
+ * `unpublished_tile` (a tile index in claim order; -1: none), and a look-back wait gives up
+ * after `spin_limit` polls (0: the default, 65536 polls of about 1 us). Lets a test force a
+ * wait to give up while every kernel still exits normally. No reference counterpart. */
+int fpscan_set_lookback_test_hook(int64_t unpublished_tile, int spin_limit);
+
+/* Launch-shape override for tuning sweeps (a tuning hook); process-wide, not synchronised
+ * with calls in flight on other threads. waves_per_row in {0,1,2,4,8,16}, ring_depth in 0..4;
  * 0 restores the built-in choice. Every setting computes the same recurrence; only the
  * grouping of fp32 partial products (and so the last-bit rounding) changes. The ring
  * depth never changes results. No reference counterpart: the
  * reference fixes its tiles at compile time (full_scan.cu:207-233). */
 int fpscan_set_launch_override(int waves_per_row, int ring_depth);
 
-/* Path selection for tests and tuning; process-wide. 0: automatic (rows: tiled for problems
+/* Path selection for tests and tuning (a test hook); process-wide, not synchronised with
+ * calls in flight. 0: automatic (rows: tiled for problems
  * of at least 512 MiB per tensor, backward from 256 MiB with rows of 128 KiB or more;
  * channel-last: tiled look-back when one pass per strip lacks strips or from 512 MiB per
  * tensor), 1: no tiled look-back (rows streamed; channel-last one

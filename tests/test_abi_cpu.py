@@ -53,7 +53,8 @@ def lib():
 def test_header_declares_the_expected_entry_points():
     names = header_functions()
     assert {"fpscan_scan_fwd", "fpscan_scan_bwd", "fpscan_workspace_bytes", "fpscan_strerror",
-            "fpscan_abi_version", "fpscan_set_launch_override", "fpscan_set_tiling"} <= set(names)
+            "fpscan_abi_version", "fpscan_set_launch_override", "fpscan_set_tiling",
+            "fpscan_lookback_overruns", "fpscan_set_lookback_test_hook"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -152,6 +153,20 @@ def test_null_pointer_rejected_and_empty_problem_accepted(lib):
     assert lib.fpscan_scan_fwd(None, None, None, 0, 4, 64, 256, 64, 0, 0, None, 0, None) == 0
     assert lib.fpscan_scan_bwd(None, None, None, None, None, 2, 0, 64, 0, 64, 2, None, 0,
                                None) == 0
+
+
+def test_lookback_test_hook_validation(lib):
+    lib.fpscan_set_lookback_test_hook.argtypes = [ctypes.c_int64, ctypes.c_int]
+    try:
+        assert lib.fpscan_set_lookback_test_hook(-1, -5) != 0  # a negative poll bound
+        assert lib.fpscan_set_lookback_test_hook(3, 16) == 0
+    finally:
+        assert lib.fpscan_set_lookback_test_hook(-1, 0) == 0  # the defaults
+
+
+def test_lookback_overruns_rejects_null(lib):
+    lib.fpscan_lookback_overruns.argtypes = [ctypes.c_void_p]
+    assert lib.fpscan_lookback_overruns(None) == header_defines()["FPSCAN_ERR_NULL"]
 
 
 def test_launch_override_validation(lib):

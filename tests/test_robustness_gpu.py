@@ -1,0 +1,223 @@
+"""GPU tests of the failure and aliasing contracts around the tiled paths.
+
+* In-place use: ``out`` may alias ``tokens`` or ``gates`` (include/fpscan_hip.h; the
+  reference's caller contract is fpscan/ops.py:55-57), on the streaming and the tiled row path
+  and at the size where tiling is the automatic choice.
+* Look-back waits that give up: a test hook keeps one tile from ever publishing its map and
+  lowers the poll bound, so the waits on it give up while every kernel still exits normally.
+  The affected tiles must come out NaN (never plausible numbers), every other value must equal
+  an unhooked run bit for bit, and the per-device counter must report the given-up waits. The
+  reference has no cross-workgroup wait (full_scan.cu:77-175 keeps every carry in one block).
+* HIP graph capture through the torch binding is refused with a RuntimeError before anything
+  is launched (the capture is begun and ended with the runtime's own calls, no graph is
+  instantiated).
+"""
+import ctypes
+
+import pytest
+import torch
+
+import bench
+import fpscan_amd
+from fpscan_amd import ops
+from scan_helpers import DEVICE, bits_equal, make_inputs
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a HIP device (MI355X)"),
+]
+
+
+class tiling:
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        ops.set_tiling(self.mode)
+
+    def __exit__(self, *exc):
+        ops.set_tiling(0)
+
+
+class lookback_hook:
+    """Tile `tile` (claim order) never publishes; waits give up after `spin` polls."""
+
+    def __init__(self, tile, spin=64):
+        self.tile, self.spin = tile, spin
+
+    def __enter__(self):
+        ops.set_lookback_test_hook(self.tile, self.spin)
+
+    def __exit__(self, *exc):
+        ops.set_lookback_test_hook(-1, 0)
+
+
+# ------------------------------------------------------------------ in-place use
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("mode", [1, 2], ids=["stream", "tiled"])
+@pytest.mark.parametrize("alias", ["tokens", "gates"])
+@pytest.mark.parametrize("reverse", [False, True], ids=["fwd", "rev"])
+def test_in_place_equals_out_of_place(dtype, mode, alias, reverse):
+    """Rows of 64 (bf16) or 128 (fp32) sub-chunks: 4 or 8 tiles per row when tiled."""
+    g, x = make_inputs(4, 8, 32768, dtype, seed=5)
+    g, x = g.to(DEVICE), x.to(DEVICE)
+    with tiling(mode):
+        want = fpscan_amd.scan_forward(g, x, reverse)
+        gi, xi = g.clone(), x.clone()
+        target = xi if alias == "tokens" else gi
+        got = fpscan_amd.scan_forward(gi, xi, reverse, out=target)
+        torch.cuda.synchronize()
+    assert got.data_ptr() == target.data_ptr()
+    assert bits_equal(got, want), f"in place on {alias} differs ({dtype}, mode {mode})"
+
+
+def test_in_place_at_the_automatic_tiling_size():
+    """bf16 (4, 1024, 65536): 512 MiB per tensor, tiled by default."""
+    B, D, L = 4, 1024, 65536
+    assert ops._load_extension().workspace_bytes(B, D, L, 2, 0) > 0  # the tiled path
+    g, x, _ = bench.make_inputs(B, D, L, torch.bfloat16, "mamba", seed=9, grad=False)
+    want = fpscan_amd.scan_forward(g, x)
+    for alias in ("tokens", "gates"):
+        gi, xi = g.clone(), x.clone()
+        target = xi if alias == "tokens" else gi
+        fpscan_amd.scan_forward(gi, xi, out=target)
+        torch.cuda.synchronize()
+        assert bits_equal(target, want), f"in place on {alias} differs"
+        del gi, xi, target
+
+
+# ------------------------------------------------------------------ look-back waits that give up
+def _tile_span(seg, tile_len, L, reverse):
+    """Element range [lo, hi) of tile `seg` of a row, in memory order."""
+    if reverse:
+        return L - (seg + 1) * tile_len, L - seg * tile_len
+    return seg * tile_len, (seg + 1) * tile_len
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("op", ["fwd", "rev", "bwd"])
+def test_row_overrun_poisons_and_is_counted(dtype, op):
+    """3 rows of 4 tiles; tile 1 (row 0, second tile in processing order) never publishes, so
+    tiles 2 and 3 of row 0 give up waiting: exactly their elements are NaN, the rest equals an
+    unhooked run, and the device counter grows by the waits that gave up."""
+    tile_len = 8192 if dtype == torch.bfloat16 else 4096  # 16 sub-chunks
+    L = 4 * tile_len
+    g, x = make_inputs(1, 3, L, dtype, seed=11)
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(12)).to(dtype)
+    g, x, go = g.to(DEVICE), x.to(DEVICE), go.to(DEVICE)
+
+    with tiling(2):
+        y = fpscan_amd.scan_forward(g, x)  # the backward's saved output, from an unhooked run
+
+        def run():
+            if op == "bwd":
+                return list(fpscan_amd.scan_backward(g, y, go))
+            return [fpscan_amd.scan_forward(g, x, op == "rev")]
+
+        want = run()
+        before = fpscan_amd.lookback_overruns()
+        with lookback_hook(1):
+            got = run()
+        torch.cuda.synchronize()
+        after = fpscan_amd.lookback_overruns()
+    assert after - before >= 2, f"given-up waits not counted ({before} -> {after})"
+    lo, hi = _tile_span(2, tile_len, L, op != "fwd")
+    lo3, hi3 = _tile_span(3, tile_len, L, op != "fwd")
+    poisoned = torch.zeros(g.shape, dtype=torch.bool)
+    poisoned[0, 0, min(lo, lo3):max(hi, hi3)] = True
+    for a, b in zip(got, want):
+        a, b = a.cpu(), b.cpu()
+        assert torch.isnan(a[poisoned]).all(), "a tile whose wait gave up must be NaN"
+        assert bits_equal(a[~poisoned], b[~poisoned]), "tiles that waited normally changed"
+    with pytest.raises(RuntimeError, match="gave up"):
+        fpscan_amd.check_lookback()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("op", ["fwd", "rev", "bwd"])
+def test_channel_last_overrun_poisons_and_is_counted(dtype, op):
+    """One chain (batch 1, 64 columns) of 16 tiles, look-back depth 5: the carry into tile k
+    composes the aggregates of tiles k-1 .. k-5 onto the end value of tile k-6. Tile 1 never
+    publishes its aggregates, so tiles 2..6 give up waiting and must be NaN; tiles 0 and 1
+    must equal an unhooked run. Once one wait of a launch has given up, the others give up at
+    once, so which later tiles are also NaN depends on timing -- but none may hold a value
+    that is neither NaN nor the unhooked one."""
+    steps = 128 if dtype == torch.bfloat16 else 64
+    L = 16 * steps
+    gen = torch.Generator().manual_seed(21)
+    g = (0.9 + 0.1 * torch.rand(1, L, 64, generator=gen)).to(dtype).to(DEVICE)
+    x = torch.randn(1, L, 64, generator=gen).to(dtype).to(DEVICE)
+    go = torch.randn(1, L, 64, generator=gen).to(dtype).to(DEVICE)
+
+    with tiling(2):
+        y = fpscan_amd.scan_forward_channel_last(g, x)
+
+        def run():
+            if op == "bwd":
+                return list(fpscan_amd.scan_backward_channel_last(g, y, go))
+            return [fpscan_amd.scan_forward_channel_last(g, x, op == "rev")]
+
+        want = run()
+        before = fpscan_amd.lookback_overruns()
+        with lookback_hook(1):
+            got = run()
+        torch.cuda.synchronize()
+        after = fpscan_amd.lookback_overruns()
+    assert after > before, f"given-up waits not counted ({before} -> {after})"
+
+    def steps_of(k0, k1):  # time steps of tiles k0 .. k1-1 in processing order
+        if op == "fwd":
+            return slice(k0 * steps, k1 * steps)
+        return slice(L - k1 * steps, L - k0 * steps)
+
+    for a, b in zip(got, want):
+        a, b = a.cpu(), b.cpu()
+        assert bits_equal(a[:, steps_of(0, 2)], b[:, steps_of(0, 2)]), "tiles 0, 1 changed"
+        assert torch.isnan(a[:, steps_of(2, 7)]).all(), "tiles 2..6 must be NaN"
+        nan = torch.isnan(a)
+        assert bits_equal(a[~nan], b[~nan]), "a value is neither NaN nor the unhooked one"
+
+
+def test_hook_off_restores_normal_runs():
+    """After the hook is cleared the tiled path publishes and waits normally again."""
+    g, x = make_inputs(1, 3, 32768, torch.bfloat16, seed=13)
+    g, x = g.to(DEVICE), x.to(DEVICE)
+    with tiling(2):
+        with lookback_hook(1):
+            fpscan_amd.scan_forward(g, x)
+        torch.cuda.synchronize()
+        before = fpscan_amd.lookback_overruns()
+        y = fpscan_amd.scan_forward(g, x)
+        torch.cuda.synchronize()
+        assert fpscan_amd.lookback_overruns() == before
+    assert not torch.isnan(y).any()
+
+
+# ------------------------------------------------------------------ graph capture is refused
+def test_graph_capture_is_refused_before_any_launch():
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch has loaded (same SONAME)
+    hip.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    g, x = make_inputs(2, 4, 1024, torch.bfloat16, seed=14)
+    g, x = g.to(DEVICE), x.to(DEVICE)
+    out = torch.empty_like(x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        relaxed = 2  # hipStreamCaptureModeRelaxed
+        assert hip.hipStreamBeginCapture(side.cuda_stream, relaxed) == 0
+        graph = ctypes.c_void_p()
+        try:
+            with pytest.raises(RuntimeError, match="graph capture"):
+                fpscan_amd.scan_forward(g, x, out=out)
+        finally:
+            assert hip.hipStreamEndCapture(side.cuda_stream, ctypes.byref(graph)) == 0
+            if graph.value:
+                hip.hipGraphDestroy(graph)
+    torch.cuda.synchronize()
+    # eager use on the same stream afterwards is unaffected
+    with torch.cuda.stream(side):
+        y = fpscan_amd.scan_forward(g, x)
+    torch.cuda.synchronize()
+    assert bits_equal(y, fpscan_amd.scan_forward(g, x))
