@@ -1,188 +1,221 @@
-"""Forward-scan latency sweep over sequence lengths: fpscan_amd against torch baselines.
+"""Forward-scan latency sweep: fpscan_amd against the torch baselines, one row per seqlen.
 
     python -m fpscan_amd.benchmark [--batch 2] [--dim 256] [--dtype float32]
                                    [--seqlens 32 64 ... 65536] [--warmup 10] [--iters 100]
                                    [--compile-assoc] [--outdir DIR]
 
-Same flags, table columns and plots as the reference's eval/benchmark.py:132-217: per seqlen
-the p50 and p90 latency of every method (HIP events, one event pair per call), fpscan's
-effective bandwidth 3 * batch * dim * seqlen * itemsize / p50, and the speedup of fpscan over
-each baseline; then latency_vs_seqlen.png and speedup_vs_seqlen.png in --outdir (default: the
-current directory). The table is a PrettyTable where that package is installed, plain aligned
-text otherwise; plots need matplotlib and are skipped with a note without it. A baseline that
-raises (for instance torch.associative_scan on a build that cannot run it eagerly) is
-disabled for the remaining seqlens, as in the reference.
+Interface kept from the reference's eval/benchmark.py, so its users find the same thing: the
+flags and their defaults, the table's columns (p50 and p90 of each method, fpscan's GB/s at
+3 * batch * dim * seqlen * itemsize bytes, the speedup of fpscan over each baseline) and the
+two plots, latency_vs_seqlen.png and speedup_vs_seqlen.png, written to --outdir (here the
+current directory by default).
+
+How it runs: every seqlen gets fresh inputs with the reference's distributions; each method
+is timed per call with a pair of HIP events around it on the current stream; a baseline that
+raises once (for example torch.associative_scan where this torch build cannot run it
+eagerly) is dropped for the rest of the sweep and its cells read nan. The table is a
+PrettyTable when that package is installed and aligned plain text otherwise; the plots need
+matplotlib and are skipped with a note without it.
 """
 from __future__ import annotations
 
 import argparse
 import math
 import os
+from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
 import torch
 
-DEFAULT_SEQLENS = [32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384, 32768, 65536]
+DEFAULT_SEQLENS = [1 << k for k in range(5, 17)]
 DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+FPSCAN = "fpscan"
 
 
+def _say(msg: str) -> None:
+    print(f"fpscan-bench: {msg}", flush=True)
+
+
+# ------------------------------------------------------------------------- measurement
 def benchmark_fn(fn: Callable[[], object], warmup: int, iters: int) -> List[float]:
-    """Per-call latency in ms: `warmup` untimed calls, then `iters` calls each bracketed by
-    HIP events on the current stream."""
+    """Latency of each of `iters` calls in ms, after `warmup` untimed calls; one HIP event
+    pair per call, recorded on the current stream (where the fpscan kernels run)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(iters)]
-    for start, end in marks:
-        start.record()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * iters)]
+    for i in range(iters):
+        events[2 * i].record()
         fn()
-        end.record()
+        events[2 * i + 1].record()
     torch.cuda.synchronize()
-    return [start.elapsed_time(end) for start, end in marks]
+    return [events[2 * i].elapsed_time(events[2 * i + 1]) for i in range(iters)]
+
+
+def _quantile(sorted_xs: Sequence[float], q: float) -> float:
+    pos = q * (len(sorted_xs) - 1)
+    below = int(math.floor(pos))
+    above = min(below + 1, len(sorted_xs) - 1)
+    return sorted_xs[below] + (pos - below) * (sorted_xs[above] - sorted_xs[below])
 
 
 def percentiles(times: Optional[Sequence[float]]) -> Tuple[float, float]:
-    """(p50, p90) with linear interpolation (torch.quantile's rule); NaNs without samples."""
+    """(p50, p90), linearly interpolated between order statistics; nan, nan when a method
+    produced no samples."""
     if not times:
         return math.nan, math.nan
-    t = torch.tensor(list(times), dtype=torch.float64)
-    return torch.quantile(t, 0.5).item(), torch.quantile(t, 0.9).item()
+    xs = sorted(float(t) for t in times)
+    return _quantile(xs, 0.5), _quantile(xs, 0.9)
 
 
 def make_inputs(batch: int, dim: int, seqlen: int, dtype: torch.dtype, device: str):
-    """eval/benchmark.py's inputs: gates 0.99 + 0.01 U(0, 1), tokens N(0, 1) / seqlen."""
-    gates = 0.99 + 0.01 * torch.rand(batch, dim, seqlen, device=device)
-    tokens = torch.randn(batch, dim, seqlen, device=device) / seqlen
+    """The reference benchmark's inputs: gates uniform in [0.99, 1), tokens N(0, 1) / seqlen,
+    drawn in fp32, rounded to `dtype`, contiguous (batch, dim, seqlen)."""
+    shape = (batch, dim, seqlen)
+    gates = torch.rand(shape, device=device).mul_(0.01).add_(0.99)
+    tokens = torch.randn(shape, device=device).div_(seqlen)
     return gates.to(dtype).contiguous(), tokens.to(dtype).contiguous()
 
 
 def effective_bandwidth_gbps(batch: int, dim: int, seqlen: int, dtype: torch.dtype,
                              p50_ms: float) -> float:
-    itemsize = torch.empty((), dtype=dtype).element_size()
-    return 3 * batch * dim * seqlen * itemsize / 1e9 / (p50_ms / 1e3)
+    """GB/s of a forward scan: it reads gates and tokens and writes the output once."""
+    moved = 3 * batch * dim * seqlen * torch.empty((), dtype=dtype).element_size()
+    return moved / (p50_ms * 1e-3) / 1e9
 
 
-def build_methods(compile_assoc: bool) -> List[Tuple[str, Callable]]:
+# ------------------------------------------------------------------------- methods
+@dataclass
+class Method:
+    name: str
+    fn: Callable[[torch.Tensor, torch.Tensor], torch.Tensor]
+    failure: Optional[str] = None  # set once the method raised; it is not run again
+
+
+def build_methods(compile_assoc: bool) -> List[Method]:
+    """fpscan first, then the baselines this torch build can run."""
     import fpscan_amd
-    from fpscan_amd.baselines import (ASSOCIATIVE_SCAN_AVAILABLE, parallel_scan_torch,
-                                      torch_associative_scan)
+    from fpscan_amd import baselines
 
-    methods: List[Tuple[str, Callable]] = [
-        ("fpscan", lambda g, x: fpscan_amd.scan_forward(g, x)),
-        ("torch parallel", lambda g, x: parallel_scan_torch(g, x)),
-    ]
-    if ASSOCIATIVE_SCAN_AVAILABLE:
-        assoc, label = torch_associative_scan, "torch.associative_scan"
-        if compile_assoc:
-            try:
-                assoc = torch.compile(torch_associative_scan)
-                label = "torch.associative_scan (compiled)"
-            except Exception as exc:  # keep the eager baseline
-                print(f"[warn] could not torch.compile associative_scan: {exc}")
-        methods.append((label, lambda g, x, f=assoc: f(g, x)))
-    else:
-        print("[info] torch.associative_scan unavailable in this torch build; "
-              "skipping that baseline.")
+    methods = [Method(FPSCAN, lambda g, x: fpscan_amd.scan_forward(g, x)),
+               Method("torch parallel", baselines.parallel_scan_torch)]
+    if not baselines.ASSOCIATIVE_SCAN_AVAILABLE:
+        _say(f"torch {torch.__version__} has no associative_scan: that column is left out")
+        return methods
+    name, fn = "torch.associative_scan", baselines.torch_associative_scan
+    if compile_assoc:
+        try:
+            fn = torch.compile(baselines.torch_associative_scan)
+            name += " (compiled)"
+        except Exception as exc:
+            _say(f"torch.compile of associative_scan failed ({exc}); timing it eagerly")
+    methods.append(Method(name, fn))
     return methods
 
 
+# ------------------------------------------------------------------------- table
 def table_fields(method_names: Sequence[str]) -> List[str]:
-    baselines = [n for n in method_names if n != "fpscan"]
-    return (["seqlen"] + [f"{n} p50 (ms)" for n in method_names]
-            + [f"{n} p90 (ms)" for n in method_names] + ["fpscan GB/s"]
-            + [f"speedup vs {n}" for n in baselines])
+    others = [n for n in method_names if n != FPSCAN]
+    return (["seqlen"]
+            + [f"{n} p50 (ms)" for n in method_names]
+            + [f"{n} p90 (ms)" for n in method_names]
+            + ["fpscan GB/s"]
+            + [f"speedup vs {n}" for n in others])
+
+
+def _cell(v) -> str:
+    return str(v) if isinstance(v, int) else f"{v:.4f}"
 
 
 def format_table(fields: Sequence[str], rows: Sequence[Sequence[float]]) -> str:
-    """The result table: PrettyTable with 4 decimals where installed, the same cells as plain
-    aligned text otherwise."""
+    """PrettyTable (4 decimals) when installed; otherwise the same cells as aligned text
+    between +---+ rules."""
     try:
         from prettytable import PrettyTable
     except ImportError:
-        PrettyTable = None
-    if PrettyTable is not None:
-        table = PrettyTable()
-        table.field_names = list(fields)
-        table.float_format = "0.4"
-        for row in rows:
-            table.add_row(list(row))
-        return str(table)
-
-    def cell(v):
-        return str(v) if isinstance(v, int) else f"{v:.4f}"
-
-    cells = [list(fields)] + [[cell(v) for v in row] for row in rows]
-    widths = [max(len(r[i]) for r in cells) for i in range(len(fields))]
-    rule = "+" + "+".join("-" * (w + 2) for w in widths) + "+"
-    lines = [rule]
-    for k, r in enumerate(cells):
-        lines.append("| " + " | ".join(c.rjust(w) for c, w in zip(r, widths)) + " |")
-        if k == 0:
-            lines.append(rule)
-    lines.append(rule)
-    return "\n".join(lines)
+        grid = [list(fields)] + [[_cell(v) for v in row] for row in rows]
+        widths = [max(len(line[c]) for line in grid) for c in range(len(fields))]
+        rule = "+".join([""] + ["-" * (w + 2) for w in widths] + [""])
+        text = [rule]
+        for n, line in enumerate(grid):
+            text.append("|" + "|".join(f" {c:>{w}} " for c, w in zip(line, widths)) + "|")
+            if n == 0:
+                text.append(rule)
+        return "\n".join(text + [rule])
+    table = PrettyTable(list(fields))
+    table.float_format = "0.4"
+    for row in rows:
+        table.add_row(list(row))
+    return table.get_string()
 
 
-def _finite(xs, ys):
-    return [(x, y) for x, y in zip(xs, ys) if y == y]
+# ------------------------------------------------------------------------- plots
+def _pyplot():
+    try:
+        import matplotlib
+    except ImportError:
+        return None
+    matplotlib.use("Agg")
+    import matplotlib.pyplot as plt
+
+    return plt
+
+
+def _line_plot(path: str, series: Dict[str, List[Tuple[int, float]]], ylabel: str, title: str,
+               log_y: bool, unity_line: bool) -> bool:
+    plt = _pyplot()
+    if plt is None:
+        _say(f"no matplotlib here, {os.path.basename(path)} not written")
+        return False
+    fig, ax = plt.subplots(figsize=(7.5, 4.5))
+    for label, points in series.items():
+        if points:
+            xs, ys = zip(*points)
+            ax.plot(xs, ys, marker="s" if label == FPSCAN else "o", linewidth=1.5, label=label)
+    if unity_line:
+        ax.axhline(1.0, color="black", linewidth=0.8, linestyle=":")
+    ax.set_xscale("log", base=2)
+    if log_y:
+        ax.set_yscale("log")
+    ax.set_xlabel("seqlen")
+    ax.set_ylabel(ylabel)
+    ax.set_title(title)
+    ax.grid(True, which="major", alpha=0.4)
+    ax.legend(loc="best")
+    fig.tight_layout()
+    fig.savefig(path, dpi=150)
+    plt.close(fig)
+    _say(f"plot written to {path}")
+    return True
+
+
+def _finite(seqlens, values):
+    return [(s, v) for s, v in zip(seqlens, values) if v == v]
 
 
 def plot_latency(seqlens, latencies: Dict[str, List[float]], names, path) -> bool:
-    try:
-        import matplotlib
-
-        matplotlib.use("Agg")
-        import matplotlib.pyplot as plt
-    except ImportError:
-        print(f"[info] matplotlib not installed; not writing {path}")
-        return False
-    fig = plt.figure(figsize=(8, 5))
-    for name in names:
-        pts = _finite(seqlens, latencies[name])
-        if pts:
-            plt.plot([p[0] for p in pts], [p[1] for p in pts], marker="o", label=name)
-    plt.xscale("log", base=2)
-    plt.yscale("log")
-    plt.xlabel("sequence length")
-    plt.ylabel("forward latency p50 (ms)")
-    plt.title("Forward scan latency vs sequence length")
-    plt.grid(True, which="both", alpha=0.3)
-    plt.legend()
-    plt.tight_layout()
-    fig.savefig(path, dpi=120)
-    plt.close(fig)
-    print(f"wrote {path}")
-    return True
+    """p50 latency of every method against seqlen, both axes logarithmic."""
+    return _line_plot(path, {n: _finite(seqlens, latencies[n]) for n in names},
+                      "p50 latency (ms)", "fpscan_amd forward scan: latency by seqlen",
+                      log_y=True, unity_line=False)
 
 
 def plot_speedup(seqlens, latencies: Dict[str, List[float]], baseline_names, path) -> bool:
-    try:
-        import matplotlib
+    """Each baseline's p50 over fpscan's, against seqlen, with the break-even line at 1."""
+    ours = latencies[FPSCAN]
+    series = {f"vs {n}": _finite(seqlens, [b / f for f, b in zip(ours, latencies[n])])
+              for n in baseline_names}
+    return _line_plot(path, series, "speedup of fpscan (x)",
+                      "fpscan_amd forward scan: speedup over baselines", log_y=False,
+                      unity_line=True)
 
-        matplotlib.use("Agg")
-        import matplotlib.pyplot as plt
-    except ImportError:
-        print(f"[info] matplotlib not installed; not writing {path}")
-        return False
-    fig = plt.figure(figsize=(8, 5))
-    base = latencies["fpscan"]
-    for name in baseline_names:
-        pts = [(s, y / b) for s, b, y in zip(seqlens, base, latencies[name]) if b == b and y == y]
-        if pts:
-            plt.plot([p[0] for p in pts], [p[1] for p in pts], marker="o", label=f"vs {name}")
-    plt.axhline(1.0, color="gray", linestyle="--", alpha=0.6)
-    plt.xscale("log", base=2)
-    plt.xlabel("sequence length")
-    plt.ylabel("speedup (baseline / fpscan)")
-    plt.title("fpscan forward speedup over baselines")
-    plt.grid(True, which="both", alpha=0.3)
-    plt.legend()
-    plt.tight_layout()
-    fig.savefig(path, dpi=120)
-    plt.close(fig)
-    print(f"wrote {path}")
-    return True
+
+# ------------------------------------------------------------------------- sweep
+@dataclass
+class Sweep:
+    names: List[str]
+    rows: List[List[float]] = field(default_factory=list)
+    latencies: Dict[str, List[float]] = field(default_factory=dict)
 
 
 def parse_args(argv=None) -> argparse.Namespace:
@@ -194,58 +227,58 @@ def parse_args(argv=None) -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--iters", type=int, default=100)
     p.add_argument("--compile-assoc", action="store_true",
-                   help="torch.compile the associative_scan baseline")
-    p.add_argument("--outdir", default=os.getcwd(), help="where the two plots go")
+                   help="time torch.compile(torch_associative_scan) instead of the eager call")
+    p.add_argument("--outdir", default=os.getcwd(), help="directory for the two PNG plots")
     return p.parse_args(argv)
 
 
+def _time_method(m: Method, gates, tokens, args) -> Optional[List[float]]:
+    if m.failure is not None:
+        return None
+    try:
+        return benchmark_fn(lambda: m.fn(gates, tokens), args.warmup, args.iters)
+    except Exception as exc:  # a baseline this build cannot run: drop it for the sweep
+        m.failure = str(exc)
+        _say(f"{m.name} raised and is dropped from the rest of the sweep: {exc}")
+        return None
+
+
 def run(args: argparse.Namespace):
-    """Runs the sweep; returns (table fields, rows, latencies per method)."""
+    """Runs the sweep; returns (table fields, rows, per-method p50 latencies)."""
     if not torch.cuda.is_available():
-        raise SystemExit("This benchmark requires a HIP device.")
+        raise SystemExit("fpscan-bench: no HIP device visible")
     dtype = DTYPES[args.dtype]
     methods = build_methods(args.compile_assoc)
-    names = [n for n, _ in methods]
-    baselines = [n for n in names if n != "fpscan"]
-    print(f"device={torch.cuda.get_device_name()}  dtype={args.dtype}  batch={args.batch}  "
-          f"dim={args.dim}  warmup={args.warmup}  iters={args.iters}")
-    latencies: Dict[str, List[float]] = {n: [] for n in names}
-    disabled: Dict[str, str] = {}
-    rows = []
+    sweep = Sweep([m.name for m in methods])
+    sweep.latencies = {n: [] for n in sweep.names}
+    _say(f"{torch.cuda.get_device_name()}, {args.dtype}, batch {args.batch}, dim {args.dim}, "
+         f"{args.warmup} warmup + {args.iters} timed calls per method")
     for seqlen in args.seqlens:
         gates, tokens = make_inputs(args.batch, args.dim, seqlen, dtype, "cuda")
-        p50s, p90s = {}, {}
-        for name, fn in methods:
-            times = None
-            if name not in disabled:
-                try:
-                    times = benchmark_fn(lambda f=fn: f(gates, tokens), args.warmup, args.iters)
-                except Exception as exc:
-                    disabled[name] = str(exc)
-                    print(f"    [disabled] {name}: {exc}")
-            p50s[name], p90s[name] = percentiles(times)
-            latencies[name].append(p50s[name])
-        fp = p50s["fpscan"]
-        gbps = (effective_bandwidth_gbps(args.batch, args.dim, seqlen, dtype, fp)
-                if fp == fp else math.nan)
-        speedups = [p50s[n] / fp if (p50s[n] == p50s[n] and fp == fp) else math.nan
-                    for n in baselines]
-        rows.append([seqlen] + [p50s[n] for n in names] + [p90s[n] for n in names] + [gbps]
-                    + speedups)
-        print(f"[{seqlen}] fpscan p50={fp:.4f}ms  "
-              + "  ".join(f"{n}x{s:.2f}" for n, s in zip(baselines, speedups)), flush=True)
-    return table_fields(names), rows, latencies
+        stats = {m.name: percentiles(_time_method(m, gates, tokens, args)) for m in methods}
+        ours = stats[FPSCAN][0]
+        speedups = [stats[n][0] / ours for n in sweep.names if n != FPSCAN]
+        gbps = effective_bandwidth_gbps(args.batch, args.dim, seqlen, dtype, ours)
+        for n in sweep.names:
+            sweep.latencies[n].append(stats[n][0])
+        sweep.rows.append([seqlen] + [stats[n][0] for n in sweep.names]
+                          + [stats[n][1] for n in sweep.names] + [gbps] + speedups)
+        others = ", ".join(f"{s:.1f}x over {n}" for n, s in
+                           zip([n for n in sweep.names if n != FPSCAN], speedups))
+        _say(f"seqlen {seqlen}: fpscan {ours:.4f} ms ({gbps:.0f} GB/s); {others}")
+        del gates, tokens
+    return table_fields(sweep.names), sweep.rows, sweep.latencies
 
 
 def main(argv=None) -> int:
     args = parse_args(argv)
     fields, rows, latencies = run(args)
-    print(format_table(fields, rows))
-    names = [f[: -len(" p50 (ms)")] for f in fields if f.endswith(" p50 (ms)")]
+    print(format_table(fields, rows), flush=True)
+    names = list(latencies)
     os.makedirs(args.outdir, exist_ok=True)
     plot_latency(args.seqlens, latencies, names,
                  os.path.join(args.outdir, "latency_vs_seqlen.png"))
-    plot_speedup(args.seqlens, latencies, [n for n in names if n != "fpscan"],
+    plot_speedup(args.seqlens, latencies, [n for n in names if n != FPSCAN],
                  os.path.join(args.outdir, "speedup_vs_seqlen.png"))
     return 0
 

@@ -85,6 +85,6 @@ def test_cli_sweep_on_the_gpu(tmp_path, capsys):
     assert benchmark.main(["--seqlens", "32", "1024", "65536", "--iters", "5", "--warmup", "2",
                            "--outdir", str(tmp_path)]) == 0
     out = capsys.readouterr().out
-    assert "fpscan p50 (ms)" in out and "[65536] fpscan p50=" in out
+    assert "fpscan p50 (ms)" in out and "seqlen 65536: fpscan" in out
     assert os.path.exists(os.path.join(tmp_path, "latency_vs_seqlen.png"))
     assert os.path.exists(os.path.join(tmp_path, "speedup_vs_seqlen.png"))
