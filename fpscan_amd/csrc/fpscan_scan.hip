@@ -1013,6 +1013,30 @@ int itemsize(int dtype) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Scratch of fpscan_scan_fwd_noalloc: the tiled path's status words and counters for up to
+// kScratchTiles tiles (2 MiB + 1152 bytes per device, held until the process ends). Host code
+// never uses the name as an address: each device's copy is found with hipGetSymbolAddress.
+constexpr int64_t kScratchTiles = 1ll << 18;
+constexpr int64_t kScratchWords = kScratchTiles + kStatusExtraWords;
+static __device__ __align__(256) uint64_t scratch[kScratchWords];
+std::atomic<uintptr_t> g_scratch_ptr[kMaxDevices];
+
+// This device's copy of `scratch`, looked up once per device with that device current.
+int scratch_on_current_device(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FPSCAN_ERR_DEVICE;
+  uintptr_t p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == 0) {
+    void* q = nullptr;
+    if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || q == nullptr)
+      return FPSCAN_ERR_DEVICE;
+    p = reinterpret_cast<uintptr_t>(q);
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *ptr = reinterpret_cast<void*>(p);
+  return FPSCAN_OK;
+}
+
 // Shared argument validation. Mirrors the reference's checks where it has them
 // (seqlen table full_scan.cu:207-233, dtype full_scan.cu:245-256) and adds the ones it
 // lacks (shape, alignment, null pointers).
@@ -1102,6 +1126,29 @@ int fpscan_scan_bwd(const void* gates, const void* out, const void* grad_out, vo
   return dispatch<kBwd>(dtype, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+int fpscan_scan_fwd_noalloc(const void* gates, const void* tokens, void* out, int64_t batch,
+                            int64_t dim, int64_t seqlen, int64_t stride_b, int64_t stride_d,
+                            int dtype, int reverse, void* stream) {
+  Args a{};
+  const int st = validate(batch, dim, seqlen, stride_b, stride_d, dtype, &a);
+  if (st != FPSCAN_OK) return st;
+  if (a.rows == 0) return FPSCAN_OK;
+  if (!gates || !tokens || !out) return FPSCAN_ERR_NULL;
+  if (!aligned16(gates) || !aligned16(tokens) || !aligned16(out)) return FPSCAN_ERR_ALIGN;
+  const TilePlan plan = plan_tiles(a.rows, seqlen, itemsize(dtype),
+                                   g_tiling.load(std::memory_order_relaxed), false);
+  if (plan.use && plan.bytes > sizeof(scratch)) return FPSCAN_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int sst = scratch_on_current_device(&ws);
+  if (sst != FPSCAN_OK) return sst;
+  a.in0 = gates;
+  a.in1 = tokens;
+  a.out0 = out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return reverse ? dispatch<kRev>(dtype, a, ws, sizeof(scratch), s)
+                 : dispatch<kFwd>(dtype, a, ws, sizeof(scratch), s);
+}
+
 int fpscan_scan_fwd_softplus(const void* z, const float* rate, const void* tokens, void* out,
                              int64_t batch, int64_t dim, int64_t seqlen, int64_t stride_b,
                              int64_t stride_d, int dtype, int reverse, void* stream) {
@@ -1167,6 +1214,9 @@ const char* fpscan_strerror(int status) {
     case FPSCAN_ERR_WORKSPACE: return "workspace too small";
     case FPSCAN_ERR_LAUNCH: return "HIP kernel launch failed";
     case FPSCAN_ERR_DEVICE: return "could not query the current HIP device";
+    case FPSCAN_ERR_SCRATCH:
+      return "problem needs more tile-status scratch than fpscan_scan_fwd_noalloc holds "
+             "(262144 tiles)";
     default: return "unknown fpscan status";
   }
 }

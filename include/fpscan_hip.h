@@ -20,7 +20,8 @@
  * fpscan_set_launch_override, fpscan_set_lookback_test_hook -- which change the path taken
  * (and so fpscan_workspace_bytes' answer and the fp32 rounding order), never the recurrence;
  * they are meant for tests and tuning sweeps and are not synchronised with calls in flight;
- * (2) per device: a count of look-back waits that gave up (fpscan_lookback_overruns).
+ * (2) per device: a count of look-back waits that gave up (fpscan_lookback_overruns), and the
+ * static scratch of fpscan_scan_fwd_noalloc.
  *
  * Look-back waits: the tiled paths chain tiles through status words and each wait for an
  * earlier tile is bounded. A wait that gives up -- which a correct launch never does, but a
@@ -78,6 +79,7 @@ extern "C" {
 #define FPSCAN_ERR_WORKSPACE 6 /* workspace smaller than fpscan_workspace_bytes() */
 #define FPSCAN_ERR_LAUNCH 7    /* hipGetLastError() reported a failure after the launch */
 #define FPSCAN_ERR_DEVICE 8    /* the current device could not be queried */
+#define FPSCAN_ERR_SCRATCH 9   /* tiled problem larger than fpscan_scan_fwd_noalloc's scratch */
 
 /* Forward or reverse scan.
  * Replaces warpscan_fwd / warpscan_forward (csrc/full_scan/full_scan.h:26-36,
@@ -89,6 +91,23 @@ int fpscan_scan_fwd(const void* gates, const void* tokens, void* out,
                     int64_t stride_b, int64_t stride_d,
                     int dtype, int reverse,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* fpscan_scan_fwd without a workspace argument and without any allocation: the tiled path's
+ * status words and claim counters live in a static device array of the library (2 MiB + 1152
+ * bytes per device, held until the process ends, found with hipGetSymbolAddress on the first
+ * call on each device), so calls make no hipMalloc/hipFree and no allocating library call.
+ * Same results and paths as fpscan_scan_fwd with a large enough workspace. A problem whose
+ * tiled plan needs more than 262144 tiles (rows * seqlen / (8192 for 2-byte types, 4096 for
+ * fp32) when it tiles) returns FPSCAN_ERR_SCRATCH. Every call on one device shares that
+ * device's scratch and clears it at the start: calls that overlap on one device (other
+ * streams, other host threads) race and must be serialised by the caller.
+ * No counterpart in the reference (its kernel needs no scratch); for callers that cannot
+ * allocate: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. */
+int fpscan_scan_fwd_noalloc(const void* gates, const void* tokens, void* out,
+                            int64_t batch, int64_t dim, int64_t seqlen,
+                            int64_t stride_b, int64_t stride_d,
+                            int dtype, int reverse, void* stream);
 
 /* Fused backward of the forward scan, given the saved forward output `out`.
  * Replaces the composition in PScan.backward (fpscan/ops.py:69-83): shifted-gate copy,

@@ -54,7 +54,8 @@ def test_header_declares_the_expected_entry_points():
     names = header_functions()
     assert {"fpscan_scan_fwd", "fpscan_scan_bwd", "fpscan_workspace_bytes", "fpscan_strerror",
             "fpscan_abi_version", "fpscan_set_launch_override", "fpscan_set_tiling",
-            "fpscan_lookback_overruns", "fpscan_set_lookback_test_hook"} <= set(names)
+            "fpscan_lookback_overruns", "fpscan_set_lookback_test_hook",
+            "fpscan_scan_fwd_noalloc"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -153,6 +154,22 @@ def test_null_pointer_rejected_and_empty_problem_accepted(lib):
     assert lib.fpscan_scan_fwd(None, None, None, 0, 4, 64, 256, 64, 0, 0, None, 0, None) == 0
     assert lib.fpscan_scan_bwd(None, None, None, None, None, 2, 0, 64, 0, 64, 2, None, 0,
                                None) == 0
+
+
+def test_noalloc_rejects_problems_beyond_its_scratch(lib):
+    """fpscan_scan_fwd_noalloc's static scratch holds 262144 tiles; a problem whose tiled plan
+    needs more fails with FPSCAN_ERR_SCRATCH before any HIP call (fake pointers are safe)."""
+    d = header_defines()
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_scan_fwd_noalloc.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                            ctypes.c_int, vp]
+    lib.fpscan_scan_fwd_noalloc.restype = ctypes.c_int
+    # fp32 (32, 1024, 65536): 32768 rows x 16 tiles = 524288 tiles, tiled by default
+    assert lib.fpscan_scan_fwd_noalloc(FAKE, FAKE, FAKE, 32, 1024, 65536, 1024 * 65536, 65536,
+                                       0, 0, None) == d["FPSCAN_ERR_SCRATCH"]
+    assert lib.fpscan_scan_fwd_noalloc(FAKE, FAKE, FAKE, 2, 4, 100, 400, 100, 0, 0,
+                                       None) == d["FPSCAN_ERR_SEQLEN"]
+    assert "262144 tiles" in lib.fpscan_strerror(d["FPSCAN_ERR_SCRATCH"]).decode()
 
 
 def test_lookback_test_hook_validation(lib):
