@@ -84,19 +84,35 @@ def _events(n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
-def time_each(fn, warmup, iters):
+def time_each(fn, warmup, iters, before=None):
     """Per-call durations (ms) from HIP event pairs on the current stream (the stream every
-    fpscan kernel is launched on)."""
+    fpscan kernel is launched on). `before`, if given, runs ahead of each call, outside the
+    events (a cache flush)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     starts, ends = _events(iters), _events(iters)
     for i in range(iters):
+        if before is not None:
+            before()
         starts[i].record()
         fn()
         ends[i].record()
     torch.cuda.synchronize()
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def cache_flusher(mib=1024):
+    """A callable that writes `mib` MiB (4x the 256 MB MALL, 32x the 32 MB of L2) so that the
+    next kernel finds none of its operands cached."""
+    buf = torch.empty(mib << 18, dtype=torch.float32, device="cuda")
+    state = {"v": 0.0}
+
+    def flush():
+        state["v"] += 1.0
+        buf.fill_(state["v"])
+
+    return flush
 
 
 def percentile(xs, q):
@@ -334,15 +350,19 @@ def bench_sweep(args):
     import fpscan_amd
 
     rows = []
-    for L in C2_SEQLENS:
+    flush = cache_flusher() if args.flush else None
+    seqlens = args.seqlens or C2_SEQLENS
+    for L in seqlens:
         gates, tokens, _ = make_inputs(2, 256, L, torch.float32, "uniform", seed=L, grad=False)
         out = torch.empty_like(tokens)
         for rev in (False, True):
-            t = time_each(lambda: fpscan_amd.scan_forward(gates, tokens, rev, out), 10, args.iters)
+            t = time_each(lambda: fpscan_amd.scan_forward(gates, tokens, rev, out), 10, args.iters,
+                          before=flush)
             p50 = percentile(t, 0.5)
             rows.append({"seqlen": L, "reverse": rev, "p50_ms": round(p50, 5),
                          "p90_ms": round(percentile(t, 0.9), 5),
-                         "gbps": round(3 * 2 * 256 * L * 4 / (p50 / 1e3) / 1e9, 1)})
+                         "gbps": round(3 * 2 * 256 * L * 4 / (p50 / 1e3) / 1e9, 1),
+                         "caches": "flushed" if args.flush else "warm"})
             print(json.dumps(rows[-1]), flush=True)
     return {"workload": "c2: fp32 B2 D256 forward/reverse sweep", "rows": rows}
 
@@ -500,10 +520,16 @@ def main():
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--flush", action="store_true",
+                    help="c2: write 1 GiB before each timed call, so operands start uncached")
+    ap.add_argument("--seqlens", type=int, nargs="+", default=None,
+                    help="c2: the seqlens to sweep (default 32 .. 65536)")
     ap.add_argument("--no-fp32", action="store_true",
                     help="c4: skip the fp32 step reported beside the bf16 headline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--launch", default=None, help="waves_per_row,ring_depth override")
+    ap.add_argument("--tiling", type=int, choices=[0, 1, 2], default=0,
+                    help="path selection: 0 automatic, 1 never tiled, 2 tiled where possible")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 5 device copies of a 1 GiB buffer: the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -518,11 +544,13 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
-    if args.launch:
+    if args.launch or args.tiling:
         import fpscan_amd.ops as ops
 
-        w, u = (int(v) for v in args.launch.split(","))
-        ops.set_launch_override(w, u)
+        if args.launch:
+            w, u = (int(v) for v in args.launch.split(","))
+            ops.set_launch_override(w, u)
+        ops.set_tiling(args.tiling)
 
     if args.calibrate_copy:
         src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")  # 1 GiB
