@@ -413,6 +413,7 @@ def bench_channel_last(args):
     import fpscan_amd
 
     B, D, L, dname, dist = WORKLOADS[args.workload[:2]]
+    B = args.batch or B
     dtype = DTYPES[args.dtype or dname]
     s = torch.empty((), dtype=dtype).element_size()
     N = B * D * L
@@ -524,6 +525,8 @@ def main():
                     help="c2: write 1 GiB before each timed call, so operands start uncached")
     ap.add_argument("--seqlens", type=int, nargs="+", default=None,
                     help="c2: the seqlens to sweep (default 32 .. 65536)")
+    ap.add_argument("--batch", type=int, default=None,
+                    help="c4cl/c5cl: override the batch (e.g. 1 for config 4's 8-GPU share)")
     ap.add_argument("--no-fp32", action="store_true",
                     help="c4: skip the fp32 step reported beside the bf16 headline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)

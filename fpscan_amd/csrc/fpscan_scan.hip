@@ -149,11 +149,13 @@ struct GateSoftplus {
     float dz[V];
     float dr[V];
   };
-  // softplus(z) = max(z, 0) + log1p(t), t = exp(-|z|) in (0, 1]. log1p(t) by Goldberg's
-  // rule: w = 1 + t, log1p(t) = t if w == 1 else log(w) * t / (w - 1) (D. Goldberg, "What
-  // every computer scientist should know about floating-point arithmetic", 1991, thm. 4),
-  // which stays accurate for small t. exp and log through the hardware's base-2
-  // instructions; sigmoid(z) = 1/w (z >= 0) or t/w.
+  // softplus(z) = max(z, 0) + ln(w), w = 1 + t, t = exp(-|z|) in (0, 1]; exp and log through
+  // the hardware's base-2 instructions, so ln(w) = ln2 * log2(w) and the gate is
+  // exp2(-rate * log2(e) * softplus(z)). Rounding w to fp32 costs softplus at most about
+  // 1e-7 absolute where t is small: below fp32 resolution in the gate (within 1e-8 of 1 there)
+  // and in d gate / d rate = -gate * softplus relative to its row sum, so no log1p correction
+  // is made. sigmoid(z) = 1/w (z >= 0) or t/w. 4 transcendental instructions (3 where only
+  // the gate is used) instead of 5 with Goldberg's log1p correction.
   __device__ static __forceinline__ void eval(float z, float rate, float& gate, float& dz,
                                               float& dr) {
     constexpr float kLog2e = 1.4426950408889634f;
@@ -161,11 +163,12 @@ struct GateSoftplus {
     const float t = __builtin_amdgcn_exp2f(-fabsf(z) * kLog2e);
     const float w = 1.0f + t;
     const float rw = __builtin_amdgcn_rcpf(w);
-    const float l1p = (w == 1.0f) ? t
-                                  : __builtin_amdgcn_logf(w) * kLn2 * t *
-                                        __builtin_amdgcn_rcpf(w - 1.0f);
-    const float sp = fmaxf(z, 0.0f) + l1p;
-    gate = __builtin_amdgcn_exp2f(-sp * rate * kLog2e);
+    float zpos;
+    // max(z, 0) in one instruction (fmaxf adds a canonicalising one); a NaN z still gives a
+    // NaN softplus, through t
+    asm("v_max_f32 %0, 0, %1" : "=v"(zpos) : "v"(z));
+    const float sp = fmaf(__builtin_amdgcn_logf(w), kLn2, zpos);
+    gate = __builtin_amdgcn_exp2f(-(sp * (rate * kLog2e)));
     const float sig = (z >= 0.0f) ? rw : t * rw;
     dz = -gate * rate * sig;
     dr = -gate * sp;
@@ -891,9 +894,10 @@ const void* long_kernel(int u) {
   // W = 16 keeps three sub-chunks in flight per wave: measured 2-5 % faster than two on
   // rows of 4 or more rounds (bf16 B8 D1024 L65536 forward 552 us against 568, backward 928
   // against 972; the backward at 77 VGPRs then runs one workgroup per CU). Other W keep at
-  // most two: their waves already multiply the bytes in flight. So do fused gates: their
-  // backward at three spills registers (128 VGPRs, measured 35 % slower).
-  if constexpr (W == 16 && !Gp::kFused) {
+  // most two: their waves already multiply the bytes in flight. So does the fused-gate
+  // backward: at three it spills registers in 2-byte types (128 VGPRs) and measured 2 %
+  // slower in fp32.
+  if constexpr (W == 16 && (!Gp::kFused || kMode != kBwd)) {
     if (u >= 3) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 3, Gp>);
   }
   if (u >= 2) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 2, Gp>);
@@ -981,7 +985,8 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   // controllers and address translation reward. Few-row problems also fill the device this
   // way (rows * 16 waves).
   int w = nsub < 16 ? nsub : 16;
-  int u_max = (w == 1 && kMode != kBwd) ? 4 : (w == 16 && !Gp::kFused ? 3 : 2);
+  int u_max = (w == 1 && kMode != kBwd) ? 4
+              : (w == 16 && (!Gp::kFused || kMode != kBwd) ? 3 : 2);
   const int ow = g_override_w.load(std::memory_order_relaxed);
   const int ou = g_override_u.load(std::memory_order_relaxed);
   if (ow > 0) w = ow <= nsub ? ow : nsub;
