@@ -219,6 +219,15 @@ __device__ __forceinline__ void make_maps(const Slot<kMode>& s, float (&al)[E::V
       be[k] = x[e];
       ysh[k] = (e == 0) ? ys_first : y[e - 1];
     }
+    if constexpr (Gp::kFused) {
+      // d loss / d z = grad_tokens * (y[t-1] * d gate / d z), and likewise for the rate: the
+      // two products are formed here, so that y[t-1] is not held across the scan
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        aux->dz[e] *= ysh[V - 1 - e];
+        aux->dr[e] *= ysh[V - 1 - e];
+      }
+    }
   } else {
 #pragma unroll
     for (int k = 0; k < V; ++k) {
@@ -263,15 +272,17 @@ __device__ __forceinline__ void finish_lane(const float (&al)[E::V], const float
   o0 = E::pack(om);
   if constexpr (kMode == kBwd) {
     float gg[V];
-#pragma unroll
-    for (int e = 0; e < V; ++e) gg[e] = om[e] * ysh[V - 1 - e];
     if constexpr (Gp::kFused) {
-      // d loss / d gate -> d loss / d z (written) and d loss / d rate (summed per row)
+      // d loss / d z (written) and d loss / d rate (summed per row); aux holds the gate
+      // derivatives already multiplied by y[t-1]
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        *rate_sum = fmaf(gg[e], aux->dr[e], *rate_sum);
-        gg[e] *= aux->dz[e];
+        *rate_sum = fmaf(om[e], aux->dr[e], *rate_sum);
+        gg[e] = om[e] * aux->dz[e];
       }
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) gg[e] = om[e] * ysh[V - 1 - e];
     }
     o1 = E::pack(gg);
   }
@@ -379,6 +390,13 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         typename Gp::template Aux<V> aux;
         make_maps<E, kMode, Gp>(ring[u], al, be, ysh, gate_next, out_prev, lane == 0, lane == 63,
                                 rate, &aux);
+        if constexpr (Gp::kFused && kMode == kBwd) {
+          // the gate derivatives are formed here, before the scan: left to the compiler, it
+          // sinks them to their use after the barrier and keeps their five inputs per element
+          // live across the scan instead of the two results
+#pragma unroll
+          for (int e = 0; e < V; ++e) asm volatile("" : "+v"(aux.dz[e]), "+v"(aux.dr[e]));
+        }
         if (kMode != kBwd && r == 0 && w == 0 && lane == 0) {
           // the first element of the row in processing order never uses its gate
           // (gates[0] forward, gates[L-1] reverse), as in full_scan.cu:96
@@ -895,8 +913,8 @@ const void* long_kernel(int u) {
   // rows of 4 or more rounds (bf16 B8 D1024 L65536 forward 552 us against 568, backward 928
   // against 972; the backward at 77 VGPRs then runs one workgroup per CU). Other W keep at
   // most two: their waves already multiply the bytes in flight. So does the fused-gate
-  // backward: at three it spills registers in 2-byte types (128 VGPRs) and measured 2 %
-  // slower in fp32.
+  // backward: at three it spills registers in bf16 (128 VGPRs) and measured 1-3 % slower
+  // than two in bf16 and fp32 (96 and 64 VGPRs at two).
   if constexpr (W == 16 && (!Gp::kFused || kMode != kBwd)) {
     if (u >= 3) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 3, Gp>);
   }
