@@ -17,6 +17,10 @@ backward kernel (the dominant one), timed alone with HIP events on the stream it
 forward plus the PScan.backward composition -- on a bounded sample of rows of the same
 inputs, on the host cores.
 
+Beside the headline, the default line also carries ``rows_f``: the fused softplus-gate scan,
+the channel-last scan and ``dimwise_forward`` at the same shape in bf16 (``--no-rows`` skips
+them).
+
 Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen sweep, forward
 and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant). Multi-GPU runs are not part
 of this build: ``--gpus N`` with N > 1 exits with a message.
@@ -299,6 +303,74 @@ def measure_training_step(B, D, L, dtype, dist, steps, warmup, workload):
     return res, (gates, tokens, grad_out)
 
 
+def rows_f_summary(iters):
+    """The next-step rows at the headline shape (B8 D1024 L65536 bf16), reported beside the
+    headline line so that each has a driver-measured figure: the fused softplus-gate scan
+    (forward and backward kernels alone, and the autograd step), the channel-last scan
+    (forward and backward, tensors (8, 65536, 1024)) and dimwise_forward. p50 over `iters`
+    calls; GB/s of algorithmic bytes (forward 3 N s, backward 5 N s, step 8 N s)."""
+    import fpscan_amd
+
+    B, D, L = 8, 1024, 65536
+    dtype = torch.bfloat16
+    s = 2
+    N = B * D * L
+
+    def gbps(nbytes, ms):
+        return round(nbytes / (ms / 1e3) / 1e9, 1)
+
+    def timed(fn, nbytes):
+        p50 = percentile(time_each(fn, 3, iters), 0.5)
+        return {"p50_ms": round(p50, 5), "gbps": gbps(nbytes, p50),
+                "hbm_frac": round(gbps(nbytes, p50) / HBM_PEAK_GBPS, 4)}
+
+    out = {"shape": "B8 D1024 L65536 bf16", "iters": iters}
+    # fused softplus gates: gates = exp(-softplus(z) * rate[d]) computed inside the kernels
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    z = torch.randn(B, D, L, generator=gen, device="cuda").to(dtype)
+    rate = 0.001 + 0.099 * torch.rand(D, generator=gen, device="cuda")
+    x = (0.1 * torch.randn(B, D, L, generator=gen, device="cuda")).to(dtype)
+    go = torch.randn(B, D, L, generator=gen, device="cuda").to(dtype)
+    y = torch.empty_like(x)
+    fused = {
+        "fwd_kernel": timed(lambda: fpscan_amd.scan_forward_softplus(z, rate, x, out=y),
+                            3 * N * s),
+        "bwd_kernel": timed(lambda: fpscan_amd.scan_backward_softplus(z, rate, y, go),
+                            5 * N * s),
+    }
+    zr, rr, xr = (t.clone().requires_grad_() for t in (z, rate, x))
+
+    def step():
+        return torch.autograd.grad(fpscan_amd.pscan_softplus(zr, rr, xr), (zr, rr, xr), go)
+
+    fused["step"] = timed(step, 8 * N * s)
+    out["softplus_fused"] = fused
+    del z, rate, x, go, y, zr, rr, xr
+    torch.cuda.empty_cache()
+    # channel-last (batch, seqlen, dim)
+    g, x, go = make_inputs(B, L, D, dtype, "mamba", seed=1)
+    y = fpscan_amd.scan_forward_channel_last(g, x)
+    o, gg, gx = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+    out["channel_last"] = {
+        "fwd": timed(lambda: fpscan_amd.scan_forward_channel_last(g, x, False, o), 3 * N * s),
+        "bwd": timed(lambda: fpscan_amd.scan_backward_channel_last(g, y, go, gg, gx), 5 * N * s),
+    }
+    del g, x, go, y, o, gg, gx
+    torch.cuda.empty_cache()
+    # dimwise_forward, in place on Bx (each call rescans the previous output: the same work)
+    G = fpscan_amd.dimwise_groups(L)
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    ax = (0.99 + 0.01 * torch.rand(B, D, L, generator=gen, device="cuda")).to(dtype)
+    bx = (torch.randn(B, D, L, generator=gen, device="cuda") / G).to(dtype)
+    bh = (torch.randn(B, D, G, generator=gen, device="cuda") / G).to(dtype)
+    wq = (0.01 * torch.rand(D, generator=gen, device="cuda")).to(dtype)
+    wk = (0.01 * torch.rand(D, generator=gen, device="cuda")).to(dtype)
+    out["dimwise"] = timed(lambda: fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk), 3 * N * s)
+    del ax, bx, bh, wq, wk
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_headline(args):
     B, D, L, dname, dist = WORKLOADS[args.workload]
     dtype = DTYPES[args.dtype or dname]
@@ -339,6 +411,8 @@ def bench_headline(args):
         f32["config"] = f"{args.workload}: pscan fwd+bwd B{B} D{D} L{L} f32"
         res["fp32"] = f32
         torch.cuda.empty_cache()
+    if args.workload == "c4" and not args.no_rows:
+        res["rows_f"] = rows_f_summary(args.steps)
     if not args.no_cpu_baseline:
         res["cpu_baseline_c1"] = cpu_baseline_c1()
     return res
@@ -529,6 +603,9 @@ def main():
                     help="c4cl/c5cl: override the batch (e.g. 1 for config 4's 8-GPU share)")
     ap.add_argument("--no-fp32", action="store_true",
                     help="c4: skip the fp32 step reported beside the bf16 headline")
+    ap.add_argument("--no-rows", action="store_true",
+                    help="c4: skip the fused-gate, channel-last and dimwise figures reported "
+                         "beside the headline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--launch", default=None, help="waves_per_row,ring_depth override")
     ap.add_argument("--tiling", type=int, choices=[0, 1, 2], default=0,
