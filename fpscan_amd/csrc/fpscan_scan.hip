@@ -115,15 +115,15 @@ struct RowRsrc {
 // sub-chunk inside the row, or kNoOffset for a ring slot past the end of the row (the loads
 // are still issued so that the wait counts stay static). Boundary values read outside the
 // row come back as 0 and are replaced by the identity where they are used.
-template <class E, int kMode, int kPolicy = kCacheNT>
+template <class E, int kMode>
 __device__ __forceinline__ void load_slot(const RowRsrc<kMode>& rr, Slot<kMode>& s,
                                           uint32_t sub_bytes, uint32_t lane_off) {
   constexpr int kSubBytes = 64 * 16;
   const uint32_t off = sub_bytes + lane_off;
-  s.v[0] = bld16<kPolicy>(rr.in0, off);
-  s.v[1] = bld16<kPolicy>(rr.in1, off);
+  s.v[0] = bld16(rr.in0, off);
+  s.v[1] = bld16(rr.in1, off);
   if constexpr (kMode == kBwd) {
-    s.v[2] = bld16<kPolicy>(rr.in2, off);
+    s.v[2] = bld16(rr.in2, off);
     s.gate_after = bld1<E>(rr.in0, sub_bytes + kSubBytes);
     s.out_before = bld1<E>(rr.in2, sub_bytes - E::kSize);
   }
@@ -324,7 +324,7 @@ __device__ __forceinline__ float segment_sum(float v, int sl) {
 // ---------------------------------------------------------------------------------------
 // Long rows: W waves per row, U sub-chunks in flight per wave.
 // ---------------------------------------------------------------------------------------
-template <class E, int kMode, int W, int U, class Gp = GatePlain, int kPolicy = kCacheNT>
+template <class E, int kMode, int W, int U, class Gp = GatePlain>
 __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Args a) {
   constexpr int V = E::V;
   constexpr int kSub = 64 * V;
@@ -368,7 +368,7 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
     Slot<kMode> ring[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      load_slot<E, kMode, kPolicy>(rr, ring[u], sub_bytes(u), lane_off);
+      load_slot<E, kMode>(rr, ring[u], sub_bytes(u), lane_off);
       __builtin_amdgcn_sched_barrier(0);  // slot u's loads before slot u+1's (wait counts)
     }
 
@@ -432,7 +432,7 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         bst16(rr.out0, sb + lane_off, o0);
         if constexpr (kMode == kBwd) bst16(rr.out1, sb + lane_off, o1);
         const uint32_t next = (r + U < nrounds) ? sub_bytes(r + U) : kNoOffset;
-        load_slot<E, kMode, kPolicy>(rr, ring[u], next, lane_off);
+        load_slot<E, kMode>(rr, ring[u], next, lane_off);
         // keep the ring order: without this the scheduler hoists the next slot's arithmetic
         // above this slot's refill, which turns every wait into a wait for all loads
         __builtin_amdgcn_sched_barrier(0);
@@ -821,7 +821,6 @@ __global__ void __launch_bounds__(256) scan_short_rows(const Args a) {
 std::atomic<int> g_override_w{0};
 std::atomic<int> g_override_u{0};
 std::atomic<int> g_tiling{0};  // 0 automatic, 1 row streaming only, 2 tiled when possible
-
 std::atomic<int64_t> g_hook_skip_publish{-1};
 std::atomic<int> g_hook_spin_limit{0};  // 0: kSpinLimit
 
@@ -843,14 +842,6 @@ constexpr int64_t kTiledMinBytes = 512ll << 20;
 // same size streaming still wins by 2-9 %.
 constexpr int64_t kTiledMinBytesBwdLongRows = 256ll << 20;
 constexpr int64_t kLongRowBytes = 128ll << 10;
-// Row-streaming calls that read at most this many bytes load their operands with the default
-// cache policy instead of the nontemporal one: operands that fit in the 256 MB MALL then stay
-// there for the next call (or are read from there when their producer has just written
-// them). Measured on MI355X through the C ABI, warm (repeated calls on the same tensors), µs
-// nontemporal / default: fp32 B2 D256 forward L32768 38.4 / 33.3, L65536 73.8 / 62.9 (256 MiB
-// read), backward L32768 62.8 / 53.6, L65536 122.7 / 129.6 (384 MiB read); bf16 B1 D1024
-// L65536 forward 72.4 / 61.0 (256 MiB), B2 forward 140.6 / 148.4 (512 MiB).
-constexpr int64_t kTemporalMaxReadBytes = 256ll << 20;
 
 struct TilePlan {
   bool use;
@@ -914,23 +905,9 @@ int launch(const void* kernel, int64_t groups, int threads, const Args& a, hipSt
 }
 
 template <class E, int kMode, int W, class Gp>
-const void* long_kernel(int u, bool temporal) {
+const void* long_kernel(int u) {
   if constexpr (W == 1) {
     if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4, Gp>);
-  }
-  // Rows of 16 sub-chunks or more whose operands fit in the MALL load them with the default
-  // cache policy (see kTemporalMaxReadBytes)
-  if constexpr (W == 16) {
-    if (temporal) {
-      if constexpr (!Gp::kFused || kMode != kBwd) {
-        if (u >= 3)
-          return reinterpret_cast<const void*>(
-              &scan_long_rows<E, kMode, W, 3, Gp, kCacheTemporal>);
-      }
-      if (u >= 2)
-        return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 2, Gp, kCacheTemporal>);
-      return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 1, Gp, kCacheTemporal>);
-    }
   }
   // W = 16 keeps three sub-chunks in flight per wave: measured 2-5 % faster than two on
   // rows of 4 or more rounds (bf16 B8 D1024 L65536 forward 552 us against 568, backward 928
@@ -946,13 +923,13 @@ const void* long_kernel(int u, bool temporal) {
 }
 
 template <class E, int kMode, class Gp>
-const void* long_kernel(int w, int u, bool temporal) {
+const void* long_kernel(int w, int u) {
   switch (w) {
-    case 1: return long_kernel<E, kMode, 1, Gp>(u, temporal);
-    case 2: return long_kernel<E, kMode, 2, Gp>(u, temporal);
-    case 4: return long_kernel<E, kMode, 4, Gp>(u, temporal);
-    case 8: return long_kernel<E, kMode, 8, Gp>(u, temporal);
-    default: return long_kernel<E, kMode, 16, Gp>(u, temporal);
+    case 1: return long_kernel<E, kMode, 1, Gp>(u);
+    case 2: return long_kernel<E, kMode, 2, Gp>(u);
+    case 4: return long_kernel<E, kMode, 4, Gp>(u);
+    case 8: return long_kernel<E, kMode, 8, Gp>(u);
+    default: return long_kernel<E, kMode, 16, Gp>(u);
   }
 }
 
@@ -1034,11 +1011,8 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (ou > 0) u_max = ou;
   const int nrounds = nsub / w;
   const int u = u_max < nrounds ? u_max : nrounds;
-  const int64_t read_bytes = a.rows * (int64_t)L * E::kSize * (kMode == kBwd ? 3 : 2);
-  const bool temporal = read_bytes <= kTemporalMaxReadBytes;
-  if (w == 1)
-    return launch(long_kernel<E, kMode, Gp>(1, u, temporal), (a.rows + 3) / 4, 256, a, stream);
-  return launch(long_kernel<E, kMode, Gp>(w, u, temporal), a.rows, 64 * w, a, stream);
+  if (w == 1) return launch(long_kernel<E, kMode, Gp>(1, u), (a.rows + 3) / 4, 256, a, stream);
+  return launch(long_kernel<E, kMode, Gp>(w, u), a.rows, 64 * w, a, stream);
 }
 
 template <int kMode, class Gp = GatePlain>

@@ -104,7 +104,6 @@ constexpr int kBwd = 2;
 // write instead of a fault.
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
 constexpr int kCacheNT = 2;             // cache-policy bit: nontemporal (streamed once)
-constexpr int kCacheTemporal = 0;       // default policy: lines may stay in L2 / MALL
 
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
@@ -113,12 +112,9 @@ __device__ __forceinline__ Rsrc row_rsrc(const void* p, int64_t row_base, int si
       const_cast<char*>(static_cast<const char*>(p)) + row_base * size, (short)0, bytes, kRsrcWord3);
 }
 
-// Every element is read once per call: the 16-byte operand loads are nontemporal by default,
-// like the stores. kCacheTemporal lets problems small enough to stay in the MALL between
-// calls be read from there by the next call.
-template <int kPolicy = kCacheNT>
+// Every element is read once: the 16-byte operand loads are nontemporal, like the stores.
 __device__ __forceinline__ u32x4 bld16(Rsrc r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kPolicy));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCacheNT));
 }
 
 __device__ __forceinline__ void bst16(Rsrc r, uint32_t off, u32x4 v) {
