@@ -87,22 +87,34 @@ __device__ __forceinline__ void st16(void* base, int64_t elem, int size, u32x4 v
 }
 
 
+// One element, as loaded: its bits (a 16-bit type zero-extended); widen_bits makes the fp32
+// value. The two are apart so that a kernel can keep the conversion next to its use.
 template <class E>
-__device__ __forceinline__ float bld1(Rsrc r, uint32_t off) {
+__device__ __forceinline__ uint32_t bld1_bits(Rsrc r, uint32_t off) {
   if constexpr (E::kSize == 4) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
   } else {
-    return E::widen16(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+}
+
+template <class E>
+__device__ __forceinline__ float widen_bits(uint32_t bits) {
+  if constexpr (E::kSize == 4) {
+    return __uint_as_float(bits);
+  } else {
+    return E::widen16((unsigned short)bits);
   }
 }
 
 // Loaded operands of one sub-chunk for one lane, plus the two wave-uniform boundary values
-// the backward needs: the gate just past the sub-chunk and the output just before it.
+// the backward needs (as loaded, see bld1_bits): the gate just past the sub-chunk and the
+// output just before it.
 template <int kMode>
 struct Slot {
   u32x4 v[kMode == kBwd ? 3 : 2];
-  float gate_after;
-  float out_before;
+  uint32_t gate_after;
+  uint32_t out_before;
 };
 
 template <int kMode>
@@ -124,8 +136,8 @@ __device__ __forceinline__ void load_slot(const RowRsrc<kMode>& rr, Slot<kMode>&
   s.v[1] = bld16(rr.in1, off);
   if constexpr (kMode == kBwd) {
     s.v[2] = bld16(rr.in2, off);
-    s.gate_after = bld1<E>(rr.in0, sub_bytes + kSubBytes);
-    s.out_before = bld1<E>(rr.in2, sub_bytes - E::kSize);
+    s.gate_after = bld1_bits<E>(rr.in0, sub_bytes + kSubBytes);
+    s.out_before = bld1_bits<E>(rr.in2, sub_bytes - E::kSize);
   }
 }
 
@@ -382,9 +394,9 @@ __global__ void __launch_bounds__(W == 1 ? 256 : 64 * W) scan_long_rows(const Ar
         if constexpr (kMode == kBwd) {
           // identity at the row edges: gates[L] = 1, y[-1] = 0
           gate_next = (sb + kSub * E::kSize < (uint32_t)row_bytes)
-                          ? Gp::gate(ring[u].gate_after, rate)
+                          ? Gp::gate(widen_bits<E>(ring[u].gate_after), rate)
                           : 1.0f;
-          out_prev = (sb > 0) ? ring[u].out_before : 0.0f;
+          out_prev = (sb > 0) ? widen_bits<E>(ring[u].out_before) : 0.0f;
         }
         float al[V], be[V], ysh[V];
         typename Gp::template Aux<V> aux;
@@ -536,8 +548,12 @@ __device__ __forceinline__ uint32_t tile_maps(const TileSlot<kMode>& ts, int nsu
   const uint32_t sb = (uint32_t)((kReverse ? nsub - 1 - j : j) * kSub * E::kSize);
   float gate_next = 1.0f, out_prev = 0.0f;
   if constexpr (kMode == kBwd) {
-    gate_next = (sb + kSub * E::kSize < (uint32_t)row_bytes) ? ts.data.gate_after : 1.0f;
-    out_prev = (sb > 0) ? ts.data.out_before : 0.0f;
+    // converted here, where the step waits for the slot's loads anyway: the empty asm keeps
+    // the compiler from converting right after the load, which would wait for it there
+    uint32_t ga = ts.data.gate_after, ob = ts.data.out_before;
+    asm volatile("" : "+v"(ga), "+v"(ob));
+    gate_next = (sb + kSub * E::kSize < (uint32_t)row_bytes) ? widen_bits<E>(ga) : 1.0f;
+    out_prev = (sb > 0) ? widen_bits<E>(ob) : 0.0f;
   }
   make_maps<E, kMode>(ts.data, al, be, ysh, gate_next, out_prev, lane == 0, lane == 63);
   if (kMode != kBwd && j == 0 && lane == 0) al[0] = 1.0f;  // full_scan.cu:96
@@ -626,132 +642,156 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
   }
   bool all_claimed = false;  // uniform: the leader has no more tiles to hand out
 
-  // The exit test sits after whole rings (surplus steps touch no memory): with an exit inside
-  // the unrolled body, the compiler's wait counts at the loop head collapse to waiting for
-  // every load in flight.
-  for (;;) {
-#pragma unroll
-    for (int u = 0; u < N; ++u) {
-      TileSlot<kMode>& cur = ring[u];
-      TileSlot<kMode>& fin = ring[(u + 2) % N];  // reduced D steps ago
-      const int hs = u % D;  // deferral slot of `fin` (and of `cur` after this step)
-      const bool cur_live = cur.tile < ntiles;  // uniform across the workgroup
+  // One step of the ring: u (a constant once the loops below are unrolled) picks the slots.
+  auto step = [&](const int u) __attribute__((always_inline)) {
+    TileSlot<kMode>& cur = ring[u];
+    TileSlot<kMode>& fin = ring[(u + 2) % N];  // reduced D steps ago
+    const int hs = u % D;  // deferral slot of `fin` (and of `cur` after this step)
+    const bool cur_live = cur.tile < ntiles;  // uniform across the workgroup
 
-      // (1) reduce the current tile (a dead tile reduces zeros and publishes nothing)
-      float al[V], be[V], ysh[V];
-      tile_maps<E, kMode, TW>(cur, nsub, row_bytes, w, lane, al, be, ysh);
-      float A, B;
-      lane_aggregate<E>(al, be, A, B);
-      wave_scan(A, B);
-      if (lane == 63) exch[w] = f32x2{A, B};
-      lds_barrier();
-      float eA = 1.0f, eB = 0.0f;
-      if (lane < TW) {
-        const f32x2 e = exch[lane];
-        eA = e.x;
-        eB = e.y;
-      }
-      combine_from_row<1>(eA, eB);
-      if constexpr (TW > 2) combine_from_row<2>(eA, eB);
-      if constexpr (TW > 4) combine_from_row<4>(eA, eB);
-      if constexpr (TW > 8) combine_from_row<8>(eA, eB);
-      const float cur_pA = (w > 0) ? readlane(eA, w - 1) : 1.0f;
-      const float cur_pB = (w > 0) ? readlane(eB, w - 1) : 0.0f;
-      const bool publisher = cur_live && w == 0 && lane == 0 && cur.tile != a.skip_publish;
-      status_store(st, publisher ? (uint32_t)(cur.tile * sizeof(uint64_t)) : kNoOffset,
-                   pack_map(readlane(eA, TW - 1), readlane(eB, TW - 1)));
+    // (1) reduce the current tile (a dead tile reduces zeros and publishes nothing)
+    float al[V], be[V], ysh[V];
+    tile_maps<E, kMode, TW>(cur, nsub, row_bytes, w, lane, al, be, ysh);
+    float A, B;
+    lane_aggregate<E>(al, be, A, B);
+    wave_scan(A, B);
+    if (lane == 63) exch[w] = f32x2{A, B};
+    lds_barrier();
+    float eA = 1.0f, eB = 0.0f;
+    if (lane < TW) {
+      const f32x2 e = exch[lane];
+      eA = e.x;
+      eB = e.y;
+    }
+    combine_from_row<1>(eA, eB);
+    if constexpr (TW > 2) combine_from_row<2>(eA, eB);
+    if constexpr (TW > 4) combine_from_row<4>(eA, eB);
+    if constexpr (TW > 8) combine_from_row<8>(eA, eB);
+    const float cur_pA = (w > 0) ? readlane(eA, w - 1) : 1.0f;
+    const float cur_pB = (w > 0) ? readlane(eB, w - 1) : 0.0f;
+    const bool publisher = cur_live && w == 0 && lane == 0 && cur.tile != a.skip_publish;
+    status_store(st, publisher ? (uint32_t)(cur.tile * sizeof(uint64_t)) : kNoOffset,
+                 pack_map(readlane(eA, TW - 1), readlane(eB, TW - 1)));
 
-      // (2) the finishing tile's carry from its predecessor words (loaded by wave 0 right
-      // after its reduce; other waves hold zeros and compute a carry nobody uses)
-      uint64_t word = held_word;
-      if (__builtin_amdgcn_ballot_w64(word == kNotPublished) != 0) {
-        // a predecessor was not published yet: poll (bounded). The poll is an atomic load,
-        // which the compiler must re-issue every iteration (a plain buffer load would be
-        // hoisted out of the loop).
-        const int64_t p = fin.tile - 64 + lane;
-        const bool in_row = p >= fin.tile - fin.seg;
-        for (int it = 0;; ++it) {
-          __builtin_amdgcn_s_sleep(1);
-          word = in_row ? __hip_atomic_load(status + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                        : 0ull;
-          if (__builtin_amdgcn_ballot_w64(word == kNotPublished) == 0) break;
-          if (it >= a.spin_limit) {
-            // only after an overrun: count it where the caller can see it, and make the
-            // tile's outputs NaN (a NaN map poisons the composed carry) instead of plausible
-            if (lane == 0) {
-              __hip_atomic_fetch_add(status + ntiles, 1ull, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-              __hip_atomic_fetch_add(&g_row_overruns, 1ull, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-            }
-            word = word == kNotPublished ? kPoisonMap : word;
-            break;
+    // (2) the finishing tile's carry from its predecessor words (loaded by wave 0 right
+    // after its reduce; other waves hold zeros and compute a carry nobody uses)
+    uint64_t word = held_word;
+    if (__builtin_amdgcn_ballot_w64(word == kNotPublished) != 0) {
+      // a predecessor was not published yet: poll (bounded). The poll is an atomic load,
+      // which the compiler must re-issue every iteration (a plain buffer load would be
+      // hoisted out of the loop).
+      const int64_t p = fin.tile - 64 + lane;
+      const bool in_row = p >= fin.tile - fin.seg;
+      for (int it = 0;; ++it) {
+        __builtin_amdgcn_s_sleep(1);
+        word = in_row ? __hip_atomic_load(status + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                      : 0ull;
+        if (__builtin_amdgcn_ballot_w64(word == kNotPublished) == 0) break;
+        if (it >= a.spin_limit) {
+          // only after an overrun: count it where the caller can see it, and make the
+          // tile's outputs NaN (a NaN map poisons the composed carry) instead of plausible
+          if (lane == 0) {
+            __hip_atomic_fetch_add(status + ntiles, 1ull, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&g_row_overruns, 1ull, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
           }
+          word = word == kNotPublished ? kPoisonMap : word;
+          break;
         }
       }
-      float mA = __uint_as_float((uint32_t)word);
-      float mB = __uint_as_float((uint32_t)(word >> 32));
-      wave_scan(mA, mB);
-      if (w == 0 && lane == 63) tile_carry = mB;
-      if (leader) {
-        const int64_t t = claims_done ? kDone : claims.resolve(pending[(u + D) % N], kBubble, kDone);
-        claims_done = t == kDone;
-        claimed = t;
-      }
-      lds_barrier();
-      const int64_t claim = __builtin_amdgcn_readfirstlane(claimed);
-      all_claimed = claim == kDone;
-      const int64_t refill = claim < ntiles ? claim : ntiles;
-
-      // (3) finish the oldest deferred tile (nothing is stored while the ring fills)
-      {
-        const float c_tile = tile_carry;
-        const float c_in = fmaf(held_pA[hs], c_tile, held_pB[hs]);
-        float pal[V], pbe[V], pys[V];
-        const uint32_t sb = tile_maps<E, kMode, TW>(fin, nsub, row_bytes, w, lane, pal, pbe, pys);
-        const float y_lane_end = fmaf(held_A[hs], c_in, held_B[hs]);
-        const float y_enter = dpp<kWaveShr1>(c_in, y_lane_end);
-        u32x4 o0, o1;
-        finish_lane<E, kMode>(pal, pbe, pys, y_enter, o0, o1);
-        const uint32_t so = have[hs] ? sb + lane_off : kNoOffset;
-        bst16(fin.rr.out0, so, o0);
-        if constexpr (kMode == kBwd) bst16(fin.rr.out1, so, o1);
-      }
-      held_A[hs] = A;
-      held_B[hs] = B;
-      held_pA[hs] = cur_pA;
-      held_pB[hs] = cur_pB;
-      have[hs] = cur_live;
-
-      // (4) wave 0: load the predecessor words of the tile finished in the next step (reduced
-      // D - 1 steps ago, or just now when D = 1) now, before the refill below: vector loads
-      // complete in issue order, so waiting for these words in the next step does not wait
-      // for the refill. Loading as late as that gives the workgroups that claimed the
-      // predecessors, just before that tile was claimed, D steps to publish them. Lanes before
-      // the row start (and all other waves) read 0: the constant map 0, the zero initial
-      // state.
-      {
-        const TileSlot<kMode>& nxt = ring[(u + 3) % N];
-        const bool nxt_live = nxt.tile < ntiles;
-        const int64_t q = nxt.tile - 64 + lane;
-        const bool mine = w == 0 && nxt_live && nxt.seg > 0 && q >= nxt.tile - nxt.seg;
-        held_word = status_load(st, mine ? (uint32_t)(q * sizeof(uint64_t)) : kNoOffset);
-      }
-      // claim the refill two steps ahead now, behind the status words and ahead of the
-      // operand loads, so that its return does not wait for them
-      pending[u] = claims.issue(st, leader && !claims_done);
-      // (5) refill the finished slot with the tile claimed two steps ago
-      tile_setup<E, kMode, TW>(a, fin, refill, ntiles, tpr_log2, w, lane_off);
-      __builtin_amdgcn_sched_barrier(0);
     }
-    // done once no claim is left, every slot is past the end and nothing is left to finish
-    // (uniform: the tile indices come from one lane)
-    bool busy = !all_claimed;
+    float mA = __uint_as_float((uint32_t)word);
+    float mB = __uint_as_float((uint32_t)(word >> 32));
+    wave_scan(mA, mB);
+    if (w == 0 && lane == 63) tile_carry = mB;
+    if (leader) {
+      const int64_t t = claims_done ? kDone : claims.resolve(pending[(u + D) % N], kBubble, kDone);
+      claims_done = t == kDone;
+      claimed = t;
+    }
+    lds_barrier();
+    const int64_t claim = __builtin_amdgcn_readfirstlane(claimed);
+    all_claimed = claim == kDone;
+    const int64_t refill = claim < ntiles ? claim : ntiles;
+
+    // (3) finish the oldest deferred tile (nothing is stored while the ring fills)
+    {
+      const float c_tile = tile_carry;
+      const float c_in = fmaf(held_pA[hs], c_tile, held_pB[hs]);
+      float pal[V], pbe[V], pys[V];
+      const uint32_t sb = tile_maps<E, kMode, TW>(fin, nsub, row_bytes, w, lane, pal, pbe, pys);
+      const float y_lane_end = fmaf(held_A[hs], c_in, held_B[hs]);
+      const float y_enter = dpp<kWaveShr1>(c_in, y_lane_end);
+      u32x4 o0, o1;
+      finish_lane<E, kMode>(pal, pbe, pys, y_enter, o0, o1);
+      const uint32_t so = have[hs] ? sb + lane_off : kNoOffset;
+      bst16(fin.rr.out0, so, o0);
+      if constexpr (kMode == kBwd) bst16(fin.rr.out1, so, o1);
+    }
+    held_A[hs] = A;
+    held_B[hs] = B;
+    held_pA[hs] = cur_pA;
+    held_pB[hs] = cur_pB;
+    have[hs] = cur_live;
+
+    // (4) wave 0: load the predecessor words of the tile finished in the next step (reduced
+    // D - 1 steps ago, or just now when D = 1) now, before the refill below: vector loads
+    // complete in issue order, so waiting for these words in the next step does not wait
+    // for the refill. Loading as late as that gives the workgroups that claimed the
+    // predecessors, just before that tile was claimed, D steps to publish them. Lanes before
+    // the row start (and all other waves) read 0: the constant map 0, the zero initial
+    // state.
+    {
+      const TileSlot<kMode>& nxt = ring[(u + 3) % N];
+      const bool nxt_live = nxt.tile < ntiles;
+      const int64_t q = nxt.tile - 64 + lane;
+      const bool mine = w == 0 && nxt_live && nxt.seg > 0 && q >= nxt.tile - nxt.seg;
+      held_word = status_load(st, mine ? (uint32_t)(q * sizeof(uint64_t)) : kNoOffset);
+    }
+    // claim the refill two steps ahead now, behind the status words and ahead of the
+    // operand loads, so that its return does not wait for them
+    pending[u] = claims.issue(st, leader && !claims_done);
+    // (5) refill the finished slot with the tile claimed two steps ago
+    tile_setup<E, kMode, TW>(a, fin, refill, ntiles, tpr_log2, w, lane_off);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Whether anything is left to finish: a deferred tile or a live slot (uniform: the tile
+  // indices come from one lane).
+  auto busy = [&]() __attribute__((always_inline)) {
+    bool b = false;
 #pragma unroll
-    for (int i = 0; i < D; ++i) busy = busy || have[i];
+    for (int i = 0; i < D; ++i) b = b || have[i];
 #pragma unroll
-    for (int i = 0; i < N; ++i) busy = busy || ring[i].tile < ntiles;
-    if (!busy) break;
+    for (int i = 0; i < N; ++i) b = b || ring[i].tile < ntiles;
+    return b;
+  };
+  // Steady state: the exit test sits after whole rings. With an exit inside the unrolled
+  // body, the compiler's wait counts at the loop head collapse to waiting for every load in
+  // flight.
+  for (;;) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) step(u);
+    if (!busy() || all_claimed) break;
+  }
+  if (!busy()) return;
+  // Drain: no tile is claimed any more, so nothing is loaded and waiting for everything in
+  // flight costs nothing; the workgroup leaves after its last finish instead of running the
+  // ring to its end (each step past it waits for the previous step's stores, about 1.7 us).
+  // The tile refilled last is finished N - 1 steps after the step that found no claim left,
+  // so at most N - 1 steps run here. The steps are written out: a loop with an exit in its
+  // body is not unrolled, and a ring slot picked at run time would put the ring in scratch.
+  static_assert(N == 4, "the drain below is written out for a ring of four slots");
+  for (;;) {
+    if (!busy()) return;
+    step(0);
+    if (!busy()) return;
+    step(1);
+    if (!busy()) return;
+    step(2);
+    if (!busy()) return;
+    step(3);
   }
 }
 
