@@ -256,13 +256,13 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 //
 // A chain is one batch's 64 consecutive columns over the whole time axis; a tile is
 // 16 R consecutive time steps of one chain (R = V: 128 steps for 2-byte types, 64 for fp32),
-// one workgroup of 16 waves. Lane r + R c of wave w holds the 16-byte vector c (V columns) of
-// time step w R + r of the tile, so every wave instruction reads R rows x 128 or 256
-// contiguous bytes. Per tile:
+// one workgroup of 16 waves. A lane of wave w holds the 16-byte vector c (V columns) of time
+// step w R + r of the tile; every wave instruction reads R rows x 128 or 256 contiguous
+// bytes, each row as 4 pieces of 16 R bytes read by consecutive lanes (the lane order is at
+// the kernel). Per tile:
 //   1. each lane turns its step into V affine maps (A, B) = (gate, token);
-//   2. a DPP scan over the R row groups of the wave (R consecutive lanes per column vector)
-//      gives each lane the inclusive map of rows 0..r of its wave, and the last row group
-//      the wave's total;
+//   2. a DPP scan over the R steps of the wave (lanes 16 / R apart in a DPP row) gives each
+//      lane the inclusive map of steps 0..r of its wave, and the last step the wave's total;
 //   3. wave totals go through LDS; wave w scans the 16 wave totals of columns 4w..4w+3 with
 //      one 16-lane DPP row each, which yields the prefix entering every wave and the tile's
 //      aggregate map per column, published at once (one 64-bit word per column);
@@ -341,7 +341,7 @@ struct ChainGroups {
   __device__ int64_t first(int g) const { return chain_lo(g) * nseg; }
 };
 
-// Time steps per tile: 16 waves of R = V row groups (one 16-byte vector of V columns per lane).
+// Time steps per tile: 16 waves of R = V steps (one 16-byte vector of V columns per lane).
 template <class E>
 constexpr int cl_tile_steps() {
   return kClTileWaves * E::V;
@@ -415,15 +415,15 @@ __device__ __forceinline__ void cl_tile_setup(const ClArgs& a, ClTile<kMode>& ts
   }
 }
 
-template <class E, int kMode, int D, int K>
+template <class E, int kMode, int D, int K, bool kStepLanes>
 __global__ void __launch_bounds__(64 * kClTileWaves)
 scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntiles) {
   constexpr int V = E::V;
-  constexpr int R = V;  // row groups per wave
+  constexpr int R = V;  // time steps per wave
   constexpr int N = D + 2;
   constexpr int kPad = 2;             // LDS row padding (f32x2), keeps 16-byte alignment
   static_assert(N % D == 0, "the unrolled ring must map each step to a fixed deferral slot");
-  static_assert(R * (kClTileCols / V) == 64, "a wave is R row groups of 64 columns");
+  static_assert(R * (kClTileCols / V) == 64, "a wave is R steps of 64 columns");
 
   __shared__ f32x2 exch[kClTileWaves][kClTileCols + kPad];  // wave totals
   __shared__ f32x2 pref[kClTileWaves][kClTileCols + kPad];  // prefix entering each wave
@@ -436,8 +436,19 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane % R;  // row group: consecutive lanes, so that the scan is a DPP one
-  const int c = lane / R;  // column group: columns V c .. V c + V - 1
+  // Lane (r, c) holds the 16-byte vector c (columns V c .. V c + V - 1) of step r of the
+  // wave. By default P = 16 / R consecutive lanes hold consecutive vectors of one step, so
+  // that each group of P lanes reads P * 16 contiguous bytes, and the R steps of a column
+  // group sit P lanes apart inside one 16-lane DPP row, so that the scan over them is
+  // full-row DPP steps. With kStepLanes, consecutive lanes hold consecutive steps (lane =
+  // r + R c) and the scan runs over aligned R-lane segments: then every lane of a quad reads
+  // another 128-byte line, which measured 2.5-3.5 % slower forward at 64 chains and more,
+  // but 5 % faster for the 2-byte backward at 128 chains (and 5-10 % slower at 32 or fewer).
+  constexpr int P = kStepLanes ? 1 : 16 / R;
+  static_assert(kStepLanes || (P * R == 16 && P * 4 * V == kClTileCols),
+                "a DPP row is P vectors of R steps");
+  const int r = kStepLanes ? lane % R : (lane / P) % R;
+  const int c = kStepLanes ? lane / R : lane % P + P * (lane / 16);
   const bool leader = threadIdx.x == 0;
   const int L = a.seqlen;
   // aggregate words, then end values (32-bit) from word nagg on, then the extra words
@@ -503,7 +514,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
   }
 
   // per deferral slot: the map from the tile's carry to this lane's value, per column (the
-  // prefix entering its wave, then its wave's row groups up to its own)
+  // prefix entering its wave, then its wave's steps up to its own)
   float held_A[D][V], held_B[D][V];
 #pragma unroll
   for (int i = 0; i < D; ++i) {
@@ -525,8 +536,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
       const bool fin_live = fin.tile < ntiles;
 
       // (1) the current tile: this lane's maps (gate, token) per column, then an inclusive
-      // scan over the R row groups of the wave (lanes R c .. R c + R - 1, one DPP segment);
-      // the last row group ends with the wave's total
+      // scan over the R steps of the wave; the last step ends with the wave's total
       float pa[V], pb[V];
       {
         E::unpack(cur.v[0], pa);
@@ -539,7 +549,16 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
 #pragma unroll
           for (int e = 0; e < V; ++e) pa[e] = 1.0f;
         }
-        segment_scan_k<R>(pa, pb, r);
+        if constexpr (kStepLanes) {
+          segment_scan_k<R>(pa, pb, r);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            if constexpr (P <= 2) combine_from_row<2>(pa[e], pb[e]);
+            if constexpr (P <= 4) combine_from_row<4>(pa[e], pb[e]);
+            combine_from_row<8>(pa[e], pb[e]);
+          }
+        }
         if (r == R - 1) {
 #pragma unroll
           for (int e = 0; e < V; ++e) exch[w][c * V + e] = f32x2{pa[e], pb[e]};
@@ -838,8 +857,11 @@ ClTilePlan plan_cl_tiles(int64_t batch, int64_t seqlen, int64_t dim, int64_t str
   return t;
 }
 
+// The 2-byte backward takes kStepLanes from this many chains (see scan_cl_tiles).
+constexpr int64_t kClStepLanesMinChains = 96;
+
 constexpr int kClMaxDevices = 64;
-std::atomic<int> g_cl_resident[kClMaxDevices][18];  // 3 types x 3 modes x 2 look-back depths
+std::atomic<int> g_cl_resident[kClMaxDevices][27];  // 3 types x 3 modes x 3 kernel variants
 
 // Workgroups of `kernel` resident at once on the current device (CUs x blocks per CU), cached
 // per device and kernel; 0 if the device cannot be queried.
@@ -864,15 +886,27 @@ int cl_resident_blocks(const void* kernel, int slot, int threads) {
 // fails (the caller then takes another path).
 template <class E, int kMode>
 int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t stream) {
-  const bool shallow =
-      kMode != kBwd &&
-      plan.chains >= (E::kSize == 4 ? kClShallowMinChainsF32 : kClShallowMinChainsHalf);
-  const void* kernel =
-      shallow ? reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsShallow>)
-              : reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep>);
+  // variants: 0 shallow look-back, 1 deep, 2 deep with kStepLanes (2-byte backward only)
+  const void* kernel = nullptr;
+  int variant = 1;
+  if constexpr (kMode != kBwd) {
+    const bool shallow =
+        plan.chains >= (E::kSize == 4 ? kClShallowMinChainsF32 : kClShallowMinChainsHalf);
+    variant = shallow ? 0 : 1;
+    kernel = shallow
+                 ? reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsShallow, false>)
+                 : reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep, false>);
+  } else if constexpr (E::kSize == 2) {
+    const bool step_lanes = plan.chains >= kClStepLanesMinChains;
+    variant = step_lanes ? 2 : 1;
+    kernel = step_lanes
+                 ? reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep, true>)
+                 : reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep, false>);
+  } else {
+    kernel = reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep, false>);
+  }
   const int threads = 64 * kClTileWaves;
-  const int resident = cl_resident_blocks(kernel, (E::kSlot * 3 + kMode) * 2 + (shallow ? 0 : 1),
-                                          threads);
+  const int resident = cl_resident_blocks(kernel, (E::kSlot * 3 + kMode) * 3 + variant, threads);
   if (resident <= 0) return -1;
   uint64_t* status = static_cast<uint64_t*>(workspace);
   int64_t ntiles = plan.ntiles;
