@@ -307,6 +307,11 @@ constexpr int kClDefer = 1;      // steps between a tile's reduce and its finish
 // 256. 7 spills registers in the half-type backward.
 constexpr int kClAggsShallow = 3;
 constexpr int kClAggsDeep = 5;
+// Below this many chains the look-back is wide (kClAggsWide = 15 aggregates, one word per
+// wave; see scan_cl_tiles): with 16 or more workgroups per chain, end(k-6) is finished in the
+// same step as tile k, so a depth of 5 waits for it about once per step.
+constexpr int kClAggsWide = kClTileWaves - 1;
+constexpr int64_t kClWideMaxChains = 48;
 constexpr int64_t kClShallowMinChainsHalf = 96;   // forward / reverse, 2-byte types
 constexpr int64_t kClShallowMinChainsF32 = 256;  // forward / reverse, fp32
 static_assert(kClTileWaves * 4 == kClTileCols, "wave w scans the totals of columns 4w..4w+3");
@@ -424,11 +429,17 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
   constexpr int kPad = 2;             // LDS row padding (f32x2), keeps 16-byte alignment
   static_assert(N % D == 0, "the unrolled ring must map each step to a fixed deferral slot");
   static_assert(R * (kClTileCols / V) == 64, "a wave is R steps of 64 columns");
+  // Wide look-back (K = 15, one predecessor word per wave): every wave loads one word per
+  // column, and the carry is composed by a 16-lane DPP scan per column in the cross-wave
+  // step. Otherwise wave 0 loads all K words and composes them serially.
+  constexpr bool kWide = K == kClTileWaves - 1;
+  static_assert(kWide || K <= 8, "narrow look-back depths are held in wave 0's registers");
 
   __shared__ f32x2 exch[kClTileWaves][kClTileCols + kPad];  // wave totals
   __shared__ f32x2 pref[kClTileWaves][kClTileCols + kPad];  // prefix entering each wave
   __shared__ f32x2 aggs[N][kClTileCols];                    // tile aggregates, by ring slot
   __shared__ float carry_in[kClTileCols];
+  __shared__ uint64_t lbw[kWide ? kClTileWaves : 1][kClTileCols];  // wide: wave w's word
   __shared__ int64_t claimed;
   __shared__ int claimed_grp;
   __shared__ int64_t first_tiles[2];
@@ -482,7 +493,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
   // (the stores, here out of range; wave 0's predecessor words and claim; the refill), so
   // that the compiler's wait counts at the loop head are the steady-state ones. Otherwise the
   // path into the loop makes it wait there for loads just issued.
-  uint64_t held_agg[K] = {};
+  uint64_t held_agg[kWide ? 1 : K] = {};  // wide: this wave's word (wave K: an end value)
   uint32_t held_end = 0;
   ClTile<kMode> ring[N];
 #pragma unroll
@@ -501,7 +512,11 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
     end_store(st, kNoOffset, 0u);
     bst16(st, kNoOffset, u32x4{0u, 0u, 0u, 0u});
     if constexpr (kMode == kBwd) bst16(st, kNoOffset, u32x4{0u, 0u, 0u, 0u});
-    if (w == 0) {
+    if constexpr (kWide) {
+      held_agg[0] = status_load(st, kNoOffset);
+      held_end = end_load(st, kNoOffset);
+      if (w == 0) pending[N - 2 + i] = claims.issue(st, leader && !claims_done);
+    } else if (w == 0) {
 #pragma unroll
       for (int j = 0; j < K; ++j) held_agg[j] = status_load(st, kNoOffset);
       held_end = end_load(st, kNoOffset);
@@ -563,6 +578,7 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
 #pragma unroll
           for (int e = 0; e < V; ++e) exch[w][c * V + e] = f32x2{pa[e], pb[e]};
         }
+        if constexpr (kWide) lbw[w][lane] = w == K ? (uint64_t)held_end : held_agg[0];
       }
 
       lds_barrier();
@@ -589,12 +605,80 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
                      pack_map(eA, eB));
       }
 
-      // (3) wave 0: the finishing tile's carry per column from its predecessors' words, and
-      // the tile's end values. The store is issued by every wave, out of range outside wave 0:
-      // a store inside a branch would leave the compiler unsure how many memory operations
-      // follow each load.
       uint32_t end_off = kNoOffset, end_word = 0;
-      if (w == 0) {
+      if constexpr (kWide) {
+        // (2b) the finishing tile's carry per column (wave w: columns 4w..4w+3): lane i of a
+        // 16-lane row takes the map of predecessor k-16+i (lane 0 the constant map of end
+        // value k-16, or of the zero state near the chain start; lanes 1..15 the aggregates
+        // of tiles k-15..k-1, or the identity before the chain start), and an inclusive DPP
+        // scan leaves lane 15 with agg(k-1) o ... o agg(k-15) o end(k-16), whose B is the
+        // carry. Missing words are polled by the lanes that need them (bounded, as below).
+        const int i = lane & 15;
+        const int col = 4 * w + (lane >> 4);
+        const int wi = K - i;  // 0..14: tile k-1-wi's aggregate; K: end value of k-16
+        const int na = min(fin.seg, K);
+        const bool need = wi < K ? wi < na : fin.seg > K;
+        uint64_t word = lbw[wi][col];
+        auto missing = [&](uint64_t v) {
+          return need && (wi < K ? v == kNotPublished : (uint32_t)v == kEndNotPublished);
+        };
+        if (__builtin_amdgcn_ballot_w64(missing(word)) != 0) {
+          const bool overran = __hip_atomic_load(status + nstatus, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT) != 0;
+          for (int it = overran ? a.spin_limit : 0;; ++it) {
+            __builtin_amdgcn_s_sleep(1);
+            if (missing(word)) {
+              if (wi < K)
+                word = __hip_atomic_load(
+                    status + (fin.tile - (int64_t)(wi + 1) * fin.nch) * kClTileCols + col,
+                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              else
+                word = __hip_atomic_load(reinterpret_cast<const uint32_t*>(status + nagg) +
+                                             (fin.tile - (int64_t)(K + 1) * fin.nch) * kClTileCols +
+                                             col,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (__builtin_amdgcn_ballot_w64(missing(word)) == 0) break;
+            if (it >= a.spin_limit) {
+              if (lane == 0) {
+                __hip_atomic_fetch_add(status + nstatus, 1ull, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(&g_cl_overruns, 1ull, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+              }
+              break;
+            }
+          }
+          // only after an overrun: a word still missing becomes NaN, as in the narrow path
+          if (missing(word)) word = wi < K ? kPoisonMap : (uint64_t)kPoisonValue;
+        }
+        float mA = 1.0f, mB = 0.0f;
+        if (wi < K) {
+          if (need) {
+            mA = __uint_as_float((uint32_t)word);
+            mB = __uint_as_float((uint32_t)(word >> 32));
+          }
+        } else {
+          mA = 0.0f;
+          mB = need ? __uint_as_float((uint32_t)word) : 0.0f;
+        }
+        combine_from_row<1>(mA, mB);
+        combine_from_row<2>(mA, mB);
+        combine_from_row<4>(mA, mB);
+        combine_from_row<8>(mA, mB);
+        // hand the carries on; the end values are read by tile k+K+1
+        if (i == 15) carry_in[col] = mB;
+        const f32x2 agg = aggs[(u + 2) % N][col];
+        if (i == 15 && fin_live && fin.seg + K + 1 < a.nseg)
+          end_off = ends_off + (uint32_t)((fin.tile * kClTileCols + col) * sizeof(uint32_t));
+        end_word = canonical_bits(fmaf(agg.x, mB, agg.y));
+      }
+
+      // (3) wave 0 (narrow look-back): the finishing tile's carry per column from its
+      // predecessors' words, and the tile's end values. The store is issued by every wave,
+      // out of range outside wave 0: a store inside a branch would leave the compiler unsure
+      // how many memory operations follow each load.
+      if constexpr (!kWide) if (w == 0) {
         const int na = min(fin.seg, K);  // aggregates composed (uniform)
         if (__builtin_amdgcn_ballot_w64(agg_missing(held_agg, na) ||
                                         (fin.seg > K && held_end == kEndNotPublished)) != 0) {
@@ -709,7 +793,20 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
       // (6) wave 0: the predecessor words of the tile finished next step (the current one),
       // loaded before the refill below (vector loads return in issue order), and the claim
       // (the leader's lane)
-      if (w == 0) {
+      if constexpr (kWide) {
+        // every wave: its one word (waves 0..K-1 an aggregate, wave K the end value)
+        const ClTile<kMode>& nxt = ring[(u + 3) % N];
+        const bool mine = nxt.tile < ntiles;
+        const int64_t p = nxt.tile - (int64_t)(w + 1) * nxt.nch;
+        held_agg[0] = status_load(
+            st, mine && w < K && w < nxt.seg ? (uint32_t)((p * kClTileCols + lane) * sizeof(uint64_t))
+                                             : kNoOffset);
+        const int64_t q = nxt.tile - (int64_t)(K + 1) * nxt.nch;
+        held_end = end_load(st, mine && w == K && nxt.seg > K
+                                    ? ends_off + (uint32_t)((q * kClTileCols + lane) * sizeof(uint32_t))
+                                    : kNoOffset);
+        if (w == 0) pending[u] = claims.issue(st, leader && !claims_done);
+      } else if (w == 0) {
         const ClTile<kMode>& nxt = ring[(u + 3) % N];
         const bool mine = nxt.tile < ntiles;
 #pragma unroll
@@ -861,7 +958,7 @@ ClTilePlan plan_cl_tiles(int64_t batch, int64_t seqlen, int64_t dim, int64_t str
 constexpr int64_t kClStepLanesMinChains = 96;
 
 constexpr int kClMaxDevices = 64;
-std::atomic<int> g_cl_resident[kClMaxDevices][27];  // 3 types x 3 modes x 3 kernel variants
+std::atomic<int> g_cl_resident[kClMaxDevices][36];  // 3 types x 3 modes x 4 kernel variants
 
 // Workgroups of `kernel` resident at once on the current device (CUs x blocks per CU), cached
 // per device and kernel; 0 if the device cannot be queried.
@@ -886,10 +983,14 @@ int cl_resident_blocks(const void* kernel, int slot, int threads) {
 // fails (the caller then takes another path).
 template <class E, int kMode>
 int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t stream) {
-  // variants: 0 shallow look-back, 1 deep, 2 deep with kStepLanes (2-byte backward only)
+  // variants: 0 shallow look-back, 1 deep, 2 deep with kStepLanes (2-byte backward only),
+  // 3 wide (few chains)
   const void* kernel = nullptr;
   int variant = 1;
-  if constexpr (kMode != kBwd) {
+  if (plan.chains < kClWideMaxChains) {
+    variant = 3;
+    kernel = reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsWide, false>);
+  } else if constexpr (kMode != kBwd) {
     const bool shallow =
         plan.chains >= (E::kSize == 4 ? kClShallowMinChainsF32 : kClShallowMinChainsHalf);
     variant = shallow ? 0 : 1;
@@ -906,7 +1007,7 @@ int run_cl_tiled(ClArgs a, const ClTilePlan& plan, void* workspace, hipStream_t 
     kernel = reinterpret_cast<const void*>(&scan_cl_tiles<E, kMode, kClDefer, kClAggsDeep, false>);
   }
   const int threads = 64 * kClTileWaves;
-  const int resident = cl_resident_blocks(kernel, (E::kSlot * 3 + kMode) * 3 + variant, threads);
+  const int resident = cl_resident_blocks(kernel, (E::kSlot * 3 + kMode) * 4 + variant, threads);
   if (resident <= 0) return -1;
   uint64_t* status = static_cast<uint64_t*>(workspace);
   int64_t ntiles = plan.ntiles;

@@ -136,12 +136,13 @@ def test_row_overrun_poisons_and_is_counted(dtype, op):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
 @pytest.mark.parametrize("op", ["fwd", "rev", "bwd"])
 def test_channel_last_overrun_poisons_and_is_counted(dtype, op):
-    """One chain (batch 1, 64 columns) of 16 tiles, look-back depth 5: the carry into tile k
-    composes the aggregates of tiles k-1 .. k-5 onto the end value of tile k-6. Tile 1 never
-    publishes its aggregates, so tiles 2..6 give up waiting and must be NaN; tiles 0 and 1
-    must equal an unhooked run. Once one wait of a launch has given up, the others give up at
-    once, so which later tiles are also NaN depends on timing -- but none may hold a value
-    that is neither NaN nor the unhooked one."""
+    """One chain (batch 1, 64 columns) of 16 tiles, so the wide look-back (few chains): the
+    carry into tile k composes the aggregates of tiles k-1 .. k-15 (back to the chain start)
+    onto the end value of tile k-16. Tile 1 never publishes its aggregates, so tiles 2..15
+    give up waiting and must be NaN (the narrow depth 5 makes that tiles 2..6; the test holds
+    either way); tiles 0 and 1 must equal an unhooked run. Once one wait of a launch has given
+    up, the others give up at once, so which later tiles are also NaN depends on timing -- but
+    none may hold a value that is neither NaN nor the unhooked one."""
     steps = 128 if dtype == torch.bfloat16 else 64
     L = 16 * steps
     gen = torch.Generator().manual_seed(21)
