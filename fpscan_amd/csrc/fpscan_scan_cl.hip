@@ -276,8 +276,8 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 // Look-back: the predecessors of tile k are the earlier tiles of its chain, k-1, k-2, ...
 // The carry into k is always composed the same way, so results do not depend on timing:
 //     carry(k) = agg(k-1) o ... o agg(k-K) applied to y_end(k-K-1)
-// (fewer maps and the zero state near the chain start; K = 3 or 5, fixed by the shape, the
-// type and the direction).
+// (fewer maps and the zero state near the chain start; K = 3, 5 or 15, fixed by the shape,
+// the type and the direction).
 // Tiles are claimed in order (Claims over chain groups: within a group all chains' tile 0,
 // then all chains' tile 1, ...), so a tile's predecessors were claimed before it. An
 // aggregate is published by a reduce, which never waits; y_end(k-K-1) by a finish, which
@@ -286,9 +286,10 @@ __global__ void __launch_bounds__(256) cl_carry(f32x2* __restrict__ ws, int64_t 
 // the row kernel, the words a finish needs are loaded one step ahead (here right after the
 // tile's reduce, kClDefer = 1) and only missing ones are polled (bounded, device-coherent).
 // The grid is every workgroup that fits on the device, so with few chains many tiles of one
-// chain are in flight and a finish often waits for y_end(k-K-1): the finishes of a chain then
-// advance K+1 tiles per publish round trip, which still beats cutting the time axis into
-// segments (measured on MI355X down to one chain).
+// chain are in flight (16 or more per chain below 16 chains per 256 workgroups), and with
+// K = 5 a finish would wait about once per step for a y_end(k-K-1) finished in the same step.
+// Below kClWideMaxChains the look-back is therefore wide: K = 15, one word per wave, so that
+// y_end(k-16) comes from the previous generation of the chain's tiles (see the kernel).
 //
 // Workspace: ntiles * 64 aggregate words (8 bytes; tile-major, one per column), ntiles * 64
 // end values (4 bytes), then the overrun word and claim counters as in the row kernel.
