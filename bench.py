@@ -307,8 +307,9 @@ def rows_f_summary(iters):
     """The next-step rows at the headline shape (B8 D1024 L65536 bf16), reported beside the
     headline line so that each has a driver-measured figure: the fused softplus-gate scan
     (forward and backward kernels alone, and the autograd step), the channel-last scan
-    (forward and backward, tensors (8, 65536, 1024)) and dimwise_forward. p50 over `iters`
-    calls; GB/s of algorithmic bytes (forward 3 N s, backward 5 N s, step 8 N s)."""
+    (forward and backward, tensors (8, 65536, 1024), and the first batch alone) and
+    dimwise_forward. p50 over `iters` calls; GB/s of algorithmic bytes (forward 3 N s,
+    backward 5 N s, step 8 N s)."""
     import fpscan_amd
 
     B, D, L = 8, 1024, 65536
@@ -355,7 +356,17 @@ def rows_f_summary(iters):
         "fwd": timed(lambda: fpscan_amd.scan_forward_channel_last(g, x, False, o), 3 * N * s),
         "bwd": timed(lambda: fpscan_amd.scan_backward_channel_last(g, y, go, gg, gx), 5 * N * s),
     }
-    del g, x, go, y, o, gg, gx
+    # the same at batch 1 (16 chains of 64 columns: one GPU's share when the batch is split
+    # over eight), which takes the wide look-back; GB/s of that batch's bytes
+    g1, x1, go1, y1, o1, gg1, gx1 = (t[:1] for t in (g, x, go, y, o, gg, gx))
+    n1 = N // B
+    out["channel_last_batch1"] = {
+        "fwd": timed(lambda: fpscan_amd.scan_forward_channel_last(g1, x1, False, o1),
+                     3 * n1 * s),
+        "bwd": timed(lambda: fpscan_amd.scan_backward_channel_last(g1, y1, go1, gg1, gx1),
+                     5 * n1 * s),
+    }
+    del g, x, go, y, o, gg, gx, g1, x1, go1, y1, o1, gg1, gx1
     torch.cuda.empty_cache()
     # dimwise_forward, in place on Bx (each call rescans the previous output: the same work)
     G = fpscan_amd.dimwise_groups(L)
