@@ -179,6 +179,56 @@ def test_channel_last_overrun_poisons_and_is_counted(dtype, op):
         assert bits_equal(a[~nan], b[~nan]), "a value is neither NaN nor the unhooked one"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("op", ["fwd", "rev", "bwd"])
+def test_channel_last_narrow_overrun_poisons_and_is_counted(dtype, op):
+    """48 chains (64 columns each) of 16 tiles, so the narrow look-back (depth 5; the wide
+    one is for fewer chains). Tile 1 in claim order, the first tile of chain 1, never
+    publishes its aggregate: tiles 1..5 of that chain give up waiting and must be NaN, as must
+    every later tile whose carry starts from one of their end values (tiles 7..11, 13..15);
+    tiles 6 and 12 start from the end values of tiles 0 and 6 and may come out right. Chain
+    1's first tile must equal an unhooked run; every other value is NaN (a wait of the launch
+    gave up after the overrun) or equal to the unhooked run, never anything else."""
+    steps = 128 if dtype == torch.bfloat16 else 64
+    L, D = 16 * steps, 48 * 64
+    gen = torch.Generator().manual_seed(23)
+    g = (0.9 + 0.1 * torch.rand(1, L, D, generator=gen)).to(dtype).to(DEVICE)
+    x = torch.randn(1, L, D, generator=gen).to(dtype).to(DEVICE)
+    go = torch.randn(1, L, D, generator=gen).to(dtype).to(DEVICE)
+
+    with tiling(2):
+        y = fpscan_amd.scan_forward_channel_last(g, x)
+
+        def run():
+            if op == "bwd":
+                return list(fpscan_amd.scan_backward_channel_last(g, y, go))
+            return [fpscan_amd.scan_forward_channel_last(g, x, op == "rev")]
+
+        want = run()
+        before = fpscan_amd.lookback_overruns()
+        with lookback_hook(1):
+            got = run()
+        torch.cuda.synchronize()
+        after = fpscan_amd.lookback_overruns()
+    assert after > before, f"given-up waits not counted ({before} -> {after})"
+
+    def steps_of(k0, k1):  # time steps of tiles k0 .. k1-1 in processing order
+        if op == "fwd":
+            return slice(k0 * steps, k1 * steps)
+        return slice(L - k1 * steps, L - k0 * steps)
+
+    chain1 = slice(64, 128)
+    for a, b in zip(got, want):
+        a, b = a.cpu(), b.cpu()
+        assert bits_equal(a[:, steps_of(0, 1), chain1], b[:, steps_of(0, 1), chain1]), \
+            "chain 1's first tile changed"
+        for k0, k1 in ((1, 6), (7, 12), (13, 16)):
+            assert torch.isnan(a[:, steps_of(k0, k1), chain1]).all(), \
+                f"chain 1's tiles {k0}..{k1 - 1} must be NaN"
+        nan = torch.isnan(a)
+        assert bits_equal(a[~nan], b[~nan]), "a value is neither NaN nor the unhooked one"
+
+
 def test_hook_off_restores_normal_runs():
     """After the hook is cleared the tiled path publishes and waits normally again."""
     g, x = make_inputs(1, 3, 32768, torch.bfloat16, seed=13)
