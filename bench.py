@@ -28,6 +28,7 @@ of this build: ``--gpus N`` with N > 1 exits with a message.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -91,18 +92,25 @@ def _events(n):
 def time_each(fn, warmup, iters, before=None):
     """Per-call durations (ms) from HIP event pairs on the current stream (the stream every
     fpscan kernel is launched on). `before`, if given, runs ahead of each call, outside the
-    events (a cache flush)."""
+    events (a cache flush). The garbage collector is paused meanwhile: a collection between
+    an event and the launch after it would count as kernel time."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     starts, ends = _events(iters), _events(iters)
-    for i in range(iters):
-        if before is not None:
-            before()
-        starts[i].record()
-        fn()
-        ends[i].record()
-    torch.cuda.synchronize()
+    gc_was_on = gc.isenabled()
+    gc.disable()
+    try:
+        for i in range(iters):
+            if before is not None:
+                before()
+            starts[i].record()
+            fn()
+            ends[i].record()
+        torch.cuda.synchronize()
+    finally:
+        if gc_was_on:
+            gc.enable()
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
@@ -247,15 +255,20 @@ def measure_training_step(B, D, L, dtype, dist, steps, warmup, workload):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    # K timed steps, bracketed by a synchronisation on both sides (one process, one GPU)
+    # K timed steps, bracketed by a synchronisation on both sides (one process, one GPU); the
+    # garbage collector is paused, as in time_each
     start, end = _events(2)
-    t0 = time.perf_counter()
-    start.record()
-    for _ in range(steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
+    gc.disable()
+    try:
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3
+    finally:
+        gc.enable()
     ms_per_step = start.elapsed_time(end) / steps
     step_p = time_each(step, 1, steps)
     del g, x
