@@ -356,6 +356,26 @@ def test_config3_b4_d512_l8192_fwd_bwd(dtype):
     check(gg, gg_ref, dtype, "c3 grad_gates")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_mid_size_rows_of_64_sub_chunks_fwd_rev_bwd(dtype):
+    """16-64 MiB tensors whose rows hold 64 sub-chunks (4 rounds of a 16-wave row) stream as
+    8-wave rows by default, forward, reverse and backward: checked against the oracle."""
+    B, D, L = (2, 256, 16384) if dtype == torch.float32 else (2, 128, 32768)
+    g, x = make_inputs(B, D, L, dtype, seed=L + 5)
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(55)).to(dtype)
+    gd, xd = g.to(DEVICE), x.to(DEVICE)
+    y = fpscan_amd.scan_forward(gd, xd)
+    y_ref = oracle.scan_f64(g, x)
+    check(y, y_ref, dtype, "mid fwd")
+    check(fpscan_amd.scan_forward(gd, xd, reverse=True), oracle.scan_f64(g, x, True), dtype,
+          "mid rev")
+    gg, gx = torch.empty_like(gd), torch.empty_like(gd)
+    fpscan_amd.scan_backward(gd, y, go.to(DEVICE), gg, gx)
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g, y.cpu().double(), go)
+    check(gx, gx_ref, dtype, "mid grad_tokens")
+    check(gg, gg_ref, dtype, "mid grad_gates")
+
+
 def _bench_inputs(batch, dim, seqlen, dtype, dist, seed):
     import bench
 
