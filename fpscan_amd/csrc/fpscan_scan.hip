@@ -1044,20 +1044,23 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
   // way (rows * 16 waves).
   int w = nsub < 16 ? nsub : 16;
   // 8 waves per row where 16 measured slower: rows of 16-64 sub-chunks (one to four 16-wave
-  // rounds) in tensors of 16-64 MiB, and in the forward and reverse rows of 16 sub-chunks
-  // from 16 MiB up. Each wave then keeps two sub-chunks in flight over 2-8 rounds instead of
-  // filling and draining its ring within one to four. Measured on MI355X (p50 of one call,
-  // same buffers, 16 waves -> 8): at 16-64 MiB forward 1-12 % faster (fp32 512 rows of
-  // L16384 20.4 -> 18.8 us, bf16 2048 rows of L8192 21.2 -> 19.0) and backward 2-13 % (the
-  // fp32 shape 31.8 -> 29.9, bf16 1024 rows of L8192 18.8 -> 17.6); forward on rows of 16
-  // sub-chunks at 128-256 MiB 3-5 % (bf16 8192 rows of L8192 68.1 -> 64.8). Elsewhere 8 waves
-  // measured slower (2-7 % on rows of 2-4 rounds at 128-256 MiB, up to 5 % below 16 MiB,
-  // where a call takes about 7 us) or even (the backward on rows of 16 at 128-256 MiB); the
-  // fused-gate kernels were not measured with 8.
+  // rounds) in tensors of 16-64 MiB; from 16 MiB up, rows of 16 sub-chunks in the forward and
+  // reverse, and rows of 16-32 sub-chunks in the fused-gate backward. Each wave then keeps two
+  // sub-chunks in flight over 2-8 rounds instead of filling and draining its ring within one
+  // to four. Measured on MI355X (p50 of one call, same buffers, 16 waves -> 8): at 16-64 MiB
+  // forward 1-12 % faster (fp32 512 rows of L16384 20.4 -> 18.8 us, bf16 2048 rows of L8192
+  // 21.2 -> 19.0) and backward 2-13 % (the fp32 shape 31.8 -> 29.9, bf16 1024 rows of L8192
+  // 18.8 -> 17.6); forward on rows of 16 sub-chunks at 128-256 MiB 3-6 % (bf16 8192 rows of
+  // L8192 68.1 -> 64.8); fused-gate backward on rows of 16-32 sub-chunks at 16-256 MiB 11-25 %
+  // (bf16 8192 rows of L8192 152.4 -> 117.4). Elsewhere 8 waves measured slower (2-9 % on
+  // rows of 2-8 rounds at 128-256 MiB, up to 5 % below 16 MiB, where a call takes about 7 us)
+  // or even (the plain backward on rows of 16 at 128-256 MiB).
   const int64_t kib = a.rows * nsub;  // tensor size: a sub-chunk is 1 KiB
-  const bool eight = (nsub >= 16 && nsub <= 64 && kib >= (16 << 10) && kib <= (64 << 10)) ||
-                     (kMode != kBwd && nsub == 16 && kib >= (16 << 10));
-  if (!Gp::kFused && eight) w = 8;
+  const bool from16 = kib >= (16 << 10);
+  const bool eight = (nsub >= 16 && nsub <= 64 && from16 && kib <= (64 << 10)) ||
+                     (kMode != kBwd && nsub == 16 && from16) ||
+                     (Gp::kFused && kMode == kBwd && nsub >= 16 && nsub <= 32 && from16);
+  if (eight) w = 8;
   int u_max = (w == 1 && kMode != kBwd) ? 4
               : (w == 16 && (!Gp::kFused || kMode != kBwd) ? 3 : 2);
   const int ow = g_override_w.load(std::memory_order_relaxed);

@@ -54,6 +54,34 @@ def test_backward_matches_oracle(dtype, seqlen):
     assert err <= max(NORM_TOL[dtype], 1e-4), f"grad_rate L{seqlen}: {err:.3e}"
 
 
+@pytest.mark.parametrize("dtype,L", [(torch.bfloat16, 8192), (torch.float32, 16384)], ids=str)
+def test_short_rows_of_16_to_64_mib_match_oracle(dtype, L):
+    """1024 rows of 16 (bf16) or 64 (fp32) sub-chunks, 16-64 MiB per tensor: shapes that
+    stream as 8-wave rows by default, forward and backward; sampled rows against the oracle,
+    every row against the 16-wave launch."""
+    z, rate, x = sp_inputs(1, 1024, L, dtype, seed=L)
+    go = torch.randn(z.shape, generator=torch.Generator().manual_seed(6)).to(dtype)
+    zd, rd, xd, god = z.to(DEVICE), rate.to(DEVICE), x.to(DEVICE), go.to(DEVICE)
+    y = fpscan_amd.scan_forward_softplus(zd, rd, xd)
+    gz, gr, gx = fpscan_amd.scan_backward_softplus(zd, rd, y, god)
+    rows = [0, 1, 511, 1022, 1023]
+    sel = lambda t: t.reshape(1024, L)[rows].reshape(1, len(rows), L).cpu()  # noqa: E731
+    check(sel(y), oracle.scan_softplus_f64(sel(z), rate[rows], sel(x)), dtype, "short rows y")
+    gz_ref, gr_ref, gx_ref = oracle.scan_bwd_softplus_f64(sel(z), rate[rows], sel(y), sel(go))
+    check(sel(gx), gx_ref, dtype, "short rows grad_tokens")
+    check(sel(gz), gz_ref, dtype, "short rows grad_z")
+    assert oracle.normwise_error(gr[rows], gr_ref) <= max(NORM_TOL[dtype], 1e-4)
+    try:
+        fpscan_amd.ops.set_launch_override(16, 0)
+        y16 = fpscan_amd.scan_forward_softplus(zd, rd, xd)
+        gz16, gr16, gx16 = fpscan_amd.scan_backward_softplus(zd, rd, y, god)
+    finally:
+        fpscan_amd.ops.set_launch_override(0, 0)
+    for got, want, what in ((y, y16, "y"), (gx, gx16, "grad_tokens"), (gz, gz16, "grad_z"),
+                            (gr, gr16, "grad_rate")):
+        assert oracle.normwise_error(got, want) <= max(NORM_TOL[dtype], 1e-5), what
+
+
 @pytest.mark.parametrize("seqlen", [64, 1024, 65536])
 def test_equals_the_unfused_composition(seqlen):
     """fp32: torch computes the gates, then the scan; the fused kernels must agree to fp32
