@@ -882,6 +882,12 @@ constexpr int64_t kTiledMinBytes = 512ll << 20;
 // same size streaming still wins by 2-9 %.
 constexpr int64_t kTiledMinBytesBwdLongRows = 256ll << 20;
 constexpr int64_t kLongRowBytes = 128ll << 10;
+// Rows of one tile (16 sub-chunks) stream as 8-wave rows, which keep up with the tiles to
+// about 1 GiB per tensor: at 512 MiB streaming measured 3-8 % faster (bf16 32768 rows of L8192
+// forward / backward 255 / 420 us against 261-278 / 438; fp32 32768 rows of L4096 256 / 428
+// against 267 / 459), at 1 GiB the tiles 2.5 % faster forward (509 against 522 us) and even
+// backward.
+constexpr int64_t kTiledMinBytesOneTileRows = 1ll << 30;
 
 struct TilePlan {
   bool use;
@@ -900,7 +906,9 @@ TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling, bool bwd
   t.tpr = (int)(nsub / kTileWaves);
   if (t.tpr > 64) return t;
   const int64_t min_bytes =
-      bwd && seqlen * size >= kLongRowBytes ? kTiledMinBytesBwdLongRows : kTiledMinBytes;
+      t.tpr == 1 ? kTiledMinBytesOneTileRows
+                 : (bwd && seqlen * size >= kLongRowBytes ? kTiledMinBytesBwdLongRows
+                                                          : kTiledMinBytes);
   if (tiling == 0 && rows * seqlen * size < min_bytes) return t;
   t.ntiles = rows * t.tpr;
   if ((t.ntiles + kStatusExtraWords) * (int64_t)sizeof(uint64_t) > INT32_MAX) return t;
