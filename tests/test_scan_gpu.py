@@ -402,6 +402,42 @@ def test_config5_b64_d4096_l256_and_transposed_layout():
     check(gg, gg_ref, torch.float32, "c5 grad_gates")
 
 
+# ------------------------------------------------------------------ rows of one sub-chunk
+# From 32768 such rows (65536 in the backward) each row gets a 64-thread block of its own; a
+# launch override sends the same call to the 4-rows-per-block launch, which computes each row
+# the same way.
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_one_row_per_block_matches_oracle_and_four_rows_per_block(dtype):
+    L = 256 if dtype == torch.float32 else 512  # one sub-chunk
+    B, D = 2, 32768 + 21  # ragged: not a multiple of 4 rows
+    g, x = make_inputs(B, D, L, dtype, seed=L + 1)
+    g[0, 100, 0] = float("nan")  # the forward's first gate of a row: never used there
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(8)).to(dtype)
+    gd, xd, god = g.to(DEVICE), x.to(DEVICE), go.to(DEVICE)
+    y = fpscan_amd.scan_forward(gd, xd)
+    yr = fpscan_amd.scan_forward(gd, xd, reverse=True)
+    gg, gx = fpscan_amd.scan_backward(gd, y, god)
+    try:
+        ops.set_launch_override(1, 1)
+        y4 = fpscan_amd.scan_forward(gd, xd)
+        yr4 = fpscan_amd.scan_forward(gd, xd, reverse=True)
+        gg4, gx4 = fpscan_amd.scan_backward(gd, y, god)
+    finally:
+        ops.set_launch_override(0, 0)
+    for got, want, what in ((y, y4, "fwd"), (yr, yr4, "rev"), (gg, gg4, "grad_gates"),
+                            (gx, gx4, "grad_tokens")):
+        assert bits_equal(got, want), f"{what}: one row per block differs from four"
+    assert torch.isfinite(y).all() and torch.isfinite(gx).all()
+    rows = torch.cat([torch.arange(0, 8), torch.arange(D - 8, D + 8),
+                      torch.arange(2 * D - 8, 2 * D)])
+    g2, x2, go2 = (t.reshape(B * D, L)[rows] for t in (g, x, go))
+    check(y.reshape(B * D, L)[rows], oracle.scan_f64(g2, x2), dtype, "one-row blocks fwd")
+    check(yr.reshape(B * D, L)[rows], oracle.scan_f64(g2, x2, True), dtype, "one-row blocks rev")
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g2, y.reshape(B * D, L)[rows].cpu(), go2)
+    check(gx.reshape(B * D, L)[rows], gx_ref, dtype, "one-row blocks grad_tokens")
+    check(gg.reshape(B * D, L)[rows], gg_ref, dtype, "one-row blocks grad_gates")
+
+
 # ------------------------------------------------------------------ tiled path (persistent
 # grid, decoupled look-back), called through the C ABI so the workspace can be inspected
 def _abi():
