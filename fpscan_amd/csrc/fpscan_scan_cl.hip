@@ -95,12 +95,12 @@ __device__ __forceinline__ Rsrc cl_rsrc(const void* p, const ClArgs& a, int64_t 
 }
 
 template <class E, int kMode, int kPhase, int U>
-__global__ void __launch_bounds__(256) scan_cl(const ClArgs a) {
+__global__ void __launch_bounds__(64) scan_cl(const ClArgs a) {
   constexpr int V = E::V;
   constexpr bool kReverse = kMode != kFwd;
 
   const int lane = threadIdx.x & 63;
-  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t task = blockIdx.x;  // one wave per block
   const int64_t ntasks = (int64_t)a.nseg * a.batch * a.strips;
   if (task >= ntasks) return;  // wave-uniform; no barrier below
   const int strip = (int)(task % a.strips);
@@ -838,7 +838,12 @@ scan_cl_tiles(const ClArgs a, uint64_t* __restrict__ status, const int64_t ntile
 // ---------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------
-constexpr int kClWaves = 4;  // independent waves per block
+// One wave (one strip task) per block: blocks of four waves put each four tasks on one CU, so
+// that 512 tasks (the fewest that take the one pass) used only 128 of the 256 CUs. Measured on
+// MI355X against four waves per block (p50 of one call, same buffers, outputs bit for bit
+// equal): 512 tasks, fp32 (32, 512, 4096) forward / backward 161.0 / 272.5 -> 135.7 / 234.7 us,
+// bf16 (64, 256, 4096) 78.0 / 135.8 -> 65.1 / 112.0; from 1024 tasks within +-2 %.
+constexpr int kClWaves = 1;
 // Below this many wave tasks in one pass the time axis is cut into segments: one wave per
 // strip and batch would leave most of the 256 CUs idle. Measured on MI355X: with 512 tasks
 // (fp32 16 x 4096 x 8192) one pass streams at 4.2 TB/s against 3.2 segmented, with 1024
