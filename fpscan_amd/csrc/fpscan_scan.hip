@@ -1087,11 +1087,11 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
     // 119.6-120.9 us, backward 224.1-233.5 -> 208.3-209.8; forward 4-10 % faster from 32 MiB,
     // backward 3-10 % from 128 MiB, even at 64 MiB and 1-3 % slower at 32 MiB; at 8 MiB
     // 7-10 % slower.
-    if constexpr (!Gp::kFused) {
-      if (nsub == 1 && ow == 0 && ou == 0 && a.rows >= (kMode == kBwd ? 64 << 10 : 32 << 10))
-        return launch(reinterpret_cast<const void*>(&scan_long_rows<E, kMode, 1, 1, Gp, 1>),
-                      a.rows, 64, a, stream);
-    }
+    // The fused-gate kernels gain as much (fp32 config 5 shape forward 125.6 -> 121.6 us,
+    // backward 224.4 -> 208.7; bf16 (64, 4096, 512) 133.3 / 223.9 -> 121.6 / 213.8).
+    if (nsub == 1 && ow == 0 && ou == 0 && a.rows >= (kMode == kBwd ? 64 << 10 : 32 << 10))
+      return launch(reinterpret_cast<const void*>(&scan_long_rows<E, kMode, 1, 1, Gp, 1>),
+                    a.rows, 64, a, stream);
     return launch(long_kernel<E, kMode, Gp>(1, u), (a.rows + 3) / 4, 256, a, stream);
   }
   return launch(long_kernel<E, kMode, Gp>(w, u), a.rows, 64 * w, a, stream);

@@ -9,7 +9,7 @@ import torch
 
 import fpscan_amd
 import oracle
-from scan_helpers import ALL_SEQLENS, DEVICE, DTYPES, NORM_TOL, check
+from scan_helpers import ALL_SEQLENS, DEVICE, DTYPES, NORM_TOL, bits_equal, check
 
 pytestmark = [
     pytest.mark.gpu,
@@ -80,6 +80,36 @@ def test_short_rows_of_16_to_64_mib_match_oracle(dtype, L):
     for got, want, what in ((y, y16, "y"), (gx, gx16, "grad_tokens"), (gz, gz16, "grad_z"),
                             (gr, gr16, "grad_rate")):
         assert oracle.normwise_error(got, want) <= max(NORM_TOL[dtype], 1e-5), what
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_one_row_per_block_matches_oracle_and_four_rows_per_block(dtype):
+    """65578 rows of one sub-chunk: each row a 64-thread block of its own, forward and
+    backward; sampled rows against the oracle, every output bit for bit against the
+    4-rows-per-block launch that a launch override selects."""
+    L = 256 if dtype == torch.float32 else 512
+    B, D = 2, 32768 + 21
+    z, rate, x = sp_inputs(B, D, L, dtype, seed=L + 3)
+    go = torch.randn(z.shape, generator=torch.Generator().manual_seed(7)).to(dtype)
+    zd, rd, xd, god = z.to(DEVICE), rate.to(DEVICE), x.to(DEVICE), go.to(DEVICE)
+    y = fpscan_amd.scan_forward_softplus(zd, rd, xd)
+    gz, gr, gx = fpscan_amd.scan_backward_softplus(zd, rd, y, god)
+    try:
+        fpscan_amd.ops.set_launch_override(1, 1)
+        y4 = fpscan_amd.scan_forward_softplus(zd, rd, xd)
+        gz4, gr4, gx4 = fpscan_amd.scan_backward_softplus(zd, rd, y, god)
+    finally:
+        fpscan_amd.ops.set_launch_override(0, 0)
+    for got, want, what in ((y, y4, "y"), (gz, gz4, "grad_z"), (gx, gx4, "grad_tokens"),
+                            (gr, gr4, "grad_rate")):
+        assert bits_equal(got, want), f"{what}: one row per block differs from four"
+    rows = [0, 1, D - 1, D, 2 * D - 1]
+    sel = lambda t: t.reshape(B * D, L)[rows].reshape(1, len(rows), L).cpu()  # noqa: E731
+    rsel = rate[[r % D for r in rows]]
+    check(sel(y), oracle.scan_softplus_f64(sel(z), rsel, sel(x)), dtype, "one-row blocks y")
+    gz_ref, _, gx_ref = oracle.scan_bwd_softplus_f64(sel(z), rsel, sel(y), sel(go))
+    check(sel(gx), gx_ref, dtype, "one-row blocks grad_tokens")
+    check(sel(gz), gz_ref, dtype, "one-row blocks grad_z")
 
 
 @pytest.mark.parametrize("seqlen", [64, 1024, 65536])
