@@ -438,6 +438,45 @@ def test_one_row_per_block_matches_oracle_and_four_rows_per_block(dtype):
     check(gg.reshape(B * D, L)[rows], gg_ref, dtype, "one-row blocks grad_gates")
 
 
+def test_one_row_per_block_with_padded_strides_through_the_c_abi():
+    """Rows of one sub-chunk in a larger buffer (stride_d = L + pad, stride_b = dim * stride_d
+    + pad2): each 64-thread block finds its row through the strides, forward and backward,
+    and the padding comes back untouched."""
+    lib = _abi()
+    B, D, L = 2, 32768 + 5, 256
+    sd, sb = L + 32, (32768 + 5) * (L + 32) + 16
+    g, x = make_inputs(B, D, L, torch.float32, seed=77)
+    go = torch.randn(B, D, L, generator=torch.Generator().manual_seed(78))
+
+    def embed(t, fill):
+        buf = torch.full((B * sb,), fill, dtype=torch.float32)
+        buf.as_strided((B, D, L), (sb, sd, 1)).copy_(t)
+        return buf.to(DEVICE)
+
+    def view(buf):
+        return buf.cpu().as_strided((B, D, L), (sb, sd, 1))
+
+    gb, xb, gob = embed(g, 7.0), embed(x, 7.0), embed(go, 7.0)
+    outb, ggb, gxb = (embed(torch.zeros_like(x), -3.0) for _ in range(3))
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.fpscan_scan_fwd(gb.data_ptr(), xb.data_ptr(), outb.data_ptr(), B, D, L, sb, sd,
+                               0, 0, None, 0, stream) == 0
+    assert lib.fpscan_scan_bwd(gb.data_ptr(), outb.data_ptr(), gob.data_ptr(), ggb.data_ptr(),
+                               gxb.data_ptr(), B, D, L, sb, sd, 0, None, 0, stream) == 0
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 4), torch.arange(D - 4, D + 4), torch.arange(2 * D - 4, 2 * D)])
+    out = view(outb).reshape(B * D, L)[rows]
+    g2, x2, go2 = (t.reshape(B * D, L)[rows] for t in (g, x, go))
+    check(out, oracle.scan_f64(g2, x2), torch.float32, "strided one-row blocks fwd")
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g2, out, go2)
+    check(view(gxb).reshape(B * D, L)[rows], gx_ref, torch.float32, "strided grad_tokens")
+    check(view(ggb).reshape(B * D, L)[rows], gg_ref, torch.float32, "strided grad_gates")
+    mask = torch.ones(B * sb, dtype=torch.bool)
+    mask.as_strided((B, D, L), (sb, sd, 1)).fill_(False)
+    for buf, what in ((outb, "out"), (ggb, "grad_gates"), (gxb, "grad_tokens")):
+        assert (buf.cpu()[mask] == -3.0).all(), f"padding of {what} was written"
+
+
 # ------------------------------------------------------------------ tiled path (persistent
 # grid, decoupled look-back), called through the C ABI so the workspace can be inspected
 def _abi():
