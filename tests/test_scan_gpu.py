@@ -438,6 +438,49 @@ def test_one_row_per_block_matches_oracle_and_four_rows_per_block(dtype):
     check(gg.reshape(B * D, L)[rows], gg_ref, dtype, "one-row blocks grad_gates")
 
 
+@pytest.mark.parametrize("dtype,L", [(torch.float32, 16384), (torch.bfloat16, 8192)], ids=str)
+def test_eight_wave_rows_with_padded_strides_through_the_c_abi(dtype, L):
+    """16-64 MiB tensors of rows with 16-64 sub-chunks (8 waves per row by default) in a
+    larger buffer: forward and backward against the oracle on sampled rows, padding
+    untouched."""
+    lib = _abi()
+    B, D = 2, 1024 if dtype == torch.bfloat16 else 256
+    vec = 16 // torch.empty((), dtype=dtype).element_size()
+    sd = L + 8 * vec
+    sb = D * sd + 4 * vec
+    g, x = make_inputs(B, D, L, dtype, seed=L + 13)
+    go = torch.randn(B, D, L, generator=torch.Generator().manual_seed(14)).to(dtype)
+
+    def embed(t, fill):
+        buf = torch.full((B * sb,), fill, dtype=dtype)
+        buf.as_strided((B, D, L), (sb, sd, 1)).copy_(t)
+        return buf.to(DEVICE)
+
+    def view(buf):
+        return buf.cpu().as_strided((B, D, L), (sb, sd, 1))
+
+    gb, xb, gob = embed(g, 7.0), embed(x, 7.0), embed(go, 7.0)
+    outb, ggb, gxb = (embed(torch.zeros_like(x), -3.0) for _ in range(3))
+    stream = torch.cuda.current_stream().cuda_stream
+    code = _CODE[dtype]
+    assert lib.fpscan_scan_fwd(gb.data_ptr(), xb.data_ptr(), outb.data_ptr(), B, D, L, sb, sd,
+                               code, 0, None, 0, stream) == 0
+    assert lib.fpscan_scan_bwd(gb.data_ptr(), outb.data_ptr(), gob.data_ptr(), ggb.data_ptr(),
+                               gxb.data_ptr(), B, D, L, sb, sd, code, None, 0, stream) == 0
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, D - 1, D, 2 * D - 1])
+    out = view(outb).reshape(B * D, L)[rows]
+    g2, x2, go2 = (t.reshape(B * D, L)[rows] for t in (g, x, go))
+    check(out, oracle.scan_f64(g2, x2), dtype, "strided 8-wave fwd")
+    gg_ref, gx_ref = oracle.scan_bwd_f64(g2, out, go2)
+    check(view(gxb).reshape(B * D, L)[rows], gx_ref, dtype, "strided 8-wave grad_tokens")
+    check(view(ggb).reshape(B * D, L)[rows], gg_ref, dtype, "strided 8-wave grad_gates")
+    mask = torch.ones(B * sb, dtype=torch.bool)
+    mask.as_strided((B, D, L), (sb, sd, 1)).fill_(False)
+    for buf, what in ((outb, "out"), (ggb, "grad_gates"), (gxb, "grad_tokens")):
+        assert (buf.cpu()[mask] == -3.0).all(), f"padding of {what} was written"
+
+
 def test_one_row_per_block_with_padded_strides_through_the_c_abi():
     """Rows of one sub-chunk in a larger buffer (stride_d = L + pad, stride_b = dim * stride_d
     + pad2): each 64-thread block finds its row through the strides, forward and backward,
