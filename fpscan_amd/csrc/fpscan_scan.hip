@@ -965,6 +965,12 @@ const void* long_kernel(int u) {
   // most two: their waves already multiply the bytes in flight. So does the fused-gate
   // backward: at three it spills registers in bf16 (128 VGPRs) and measured 1-3 % slower
   // than two in bf16 and fp32 (96 and 64 VGPRs at two).
+  // The forward and reverse keep four on rows of 8 rounds or more (the caller's choice of u):
+  // 1-3 % faster than three (fp32 B2 D256 L32768 forward 38.4 -> 37.4 us, fused-gate bf16
+  // B8 D1024 L65536 556.4 -> 547.6), within 64 VGPRs.
+  if constexpr (W == 16 && kMode != kBwd) {
+    if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4, Gp>);
+  }
   if constexpr (W == 16 && (!Gp::kFused || kMode != kBwd)) {
     if (u >= 3) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 3, Gp>);
   }
@@ -1072,6 +1078,7 @@ int run(const Args& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
                      (Gp::kFused && kMode == kBwd && nsub >= 16 && nsub <= 32 && from16);
   if (eight) w = 8;
   int u_max = (w == 1 && kMode != kBwd) ? 4
+              : (w == 16 && kMode != kBwd && nsub >= 8 * 16) ? 4
               : (w == 16 && (!Gp::kFused || kMode != kBwd) ? 3 : 2);
   const int ow = g_override_w.load(std::memory_order_relaxed);
   const int ou = g_override_u.load(std::memory_order_relaxed);
