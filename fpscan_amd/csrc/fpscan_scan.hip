@@ -961,13 +961,13 @@ const void* long_kernel(int u) {
   }
   // W = 16 keeps three sub-chunks in flight per wave: measured 2-5 % faster than two on
   // rows of 4 or more rounds (bf16 B8 D1024 L65536 forward 552 us against 568, backward 928
-  // against 972; the backward at 77 VGPRs then runs one workgroup per CU). Other W keep at
-  // most two: their waves already multiply the bytes in flight. So does the fused-gate
-  // backward: at three it spills registers in bf16 (128 VGPRs) and measured 1-3 % slower
-  // than two in bf16 and fp32 (96 and 64 VGPRs at two).
-  // The forward and reverse keep four on rows of 8 rounds or more (the caller's choice of u):
-  // 1-3 % faster than three (fp32 B2 D256 L32768 forward 38.4 -> 37.4 us, fused-gate bf16
-  // B8 D1024 L65536 556.4 -> 547.6), within 64 VGPRs.
+  // against 972). The forward and reverse keep four on rows of 8 rounds or more (the
+  // caller's choice of u): 1-3 % faster than three (fp32 B2 D256 L32768 forward 38.4 -> 37.4
+  // us, fused-gate bf16 B8 D1024 L65536 556.4 -> 547.6), within 64 VGPRs; the backward at
+  // four (79-97 VGPRs) measured 0.5-1 % slower than three. Other W keep at most two: their
+  // waves already multiply the bytes in flight. So does the fused-gate backward: at three it
+  // spills registers in bf16 (128 VGPRs) and measured 1-3 % slower than two in bf16 and fp32
+  // (96 and 64 VGPRs at two).
   if constexpr (W == 16 && kMode != kBwd) {
     if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4, Gp>);
   }
