@@ -316,6 +316,13 @@ def measure_training_step(B, D, L, dtype, dist, steps, warmup, workload):
     return res, (gates, tokens, grad_out)
 
 
+# Freed device memory stays in torch's cache for the whole run: returning it to the driver
+# (torch.cuda.empty_cache) between measurements made the next measurement run slow while the
+# driver wiped the released memory in the background (measured: a 10-17 ms stall inside the
+# fp32 step or its backward-kernel timing in half of such runs, and the fused-gate forward
+# that follows the fp32 step 1.8 % slower; none without the release). A default run reserves
+# at most 18 GiB of the 288.
+#
 # Untimed calls before each separately timed kernel or step of the side workloads: the first
 # few dozen milliseconds of GPU work after a pause run a few per cent slow (measured: the
 # channel-last forward's first 20 calls 587 us, then 566-568, the same as its reverse).
@@ -366,7 +373,6 @@ def rows_f_summary(iters):
     fused["step"] = timed(step, 8 * N * s)
     out["softplus_fused"] = fused
     del z, rate, x, go, y, zr, rr, xr
-    torch.cuda.empty_cache()
     # channel-last (batch, seqlen, dim)
     g, x, go = make_inputs(B, L, D, dtype, "mamba", seed=1)
     y = fpscan_amd.scan_forward_channel_last(g, x)
@@ -386,7 +392,6 @@ def rows_f_summary(iters):
                      5 * n1 * s),
     }
     del g, x, go, y, o, gg, gx, g1, x1, go1, y1, o1, gg1, gx1
-    torch.cuda.empty_cache()
     # dimwise_forward, in place on Bx (each call rescans the previous output: the same work)
     G = fpscan_amd.dimwise_groups(L)
     gen = torch.Generator(device="cuda").manual_seed(2)
@@ -397,7 +402,6 @@ def rows_f_summary(iters):
     wk = (0.01 * torch.rand(D, generator=gen, device="cuda")).to(dtype)
     out["dimwise"] = timed(lambda: fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk), 3 * N * s)
     del ax, bx, bh, wq, wk
-    torch.cuda.empty_cache()
     return out
 
 
@@ -432,7 +436,6 @@ def bench_headline(args):
     else:
         res["cpu_baseline"] = cpu_baseline(*inputs, args.cpu_seconds)
     del inputs
-    torch.cuda.empty_cache()
     if args.workload == "c4" and dtype != torch.float32 and not args.no_fp32:
         # the north star's second dtype, fp32 (the reference's only published dtype): the same
         # step at the same shape, reported beside the headline line's bf16 figures
@@ -440,7 +443,6 @@ def bench_headline(args):
                                        args.workload)
         f32["config"] = f"{args.workload}: pscan fwd+bwd B{B} D{D} L{L} f32"
         res["fp32"] = f32
-        torch.cuda.empty_cache()
     if args.workload == "c4" and not args.no_rows:
         res["rows_f"] = rows_f_summary(args.steps)
     if not args.no_cpu_baseline:
