@@ -225,12 +225,12 @@ def cpu_baseline_c1(warmup=3, iters=20):
 def load_traffic(workload, dtype_short):
     """HBM bytes per backward launch measured by rocprofv3 PMC counters (FETCH_SIZE,
     WRITE_SIZE, scaled by a copy kernel of known size), committed under profiles/."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        f"pmc_traffic_{workload}_{dtype_short}.json")
+    rel = os.path.join("profiles", f"pmc_traffic_{workload}_{dtype_short}.json")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), rel)
     try:
         with open(path) as f:
             d = json.load(f)
-        return d.get("bwd_bytes_per_launch"), os.path.relpath(path)
+        return d.get("bwd_bytes_per_launch"), rel  # relative to the repository root
     except (OSError, ValueError):
         return None, None
 
