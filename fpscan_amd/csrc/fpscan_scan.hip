@@ -161,13 +161,18 @@ struct GateSoftplus {
     float dz[V];
     float dr[V];
   };
-  // softplus(z) = max(z, 0) + ln(w), w = 1 + t, t = exp(-|z|) in (0, 1]; exp and log through
-  // the hardware's base-2 instructions, so ln(w) = ln2 * log2(w) and the gate is
-  // exp2(-rate * log2(e) * softplus(z)). Rounding w to fp32 costs softplus at most about
-  // 1e-7 absolute where t is small: below fp32 resolution in the gate (within 1e-8 of 1 there)
-  // and in d gate / d rate = -gate * softplus relative to its row sum, so no log1p correction
-  // is made. sigmoid(z) = 1/w (z >= 0) or t/w. 4 transcendental instructions (3 where only
-  // the gate is used) instead of 5 with Goldberg's log1p correction.
+  // softplus(z) = max(z, 0) + ln(1 + t), t = exp(-|z|) in (0, 1]; exp and log through the
+  // hardware's base-2 instructions, so ln(w) = ln2 * log2(w) and the gate is
+  // exp2(-rate * log2(e) * softplus(z)). sigmoid(z) = 1/w (z >= 0) or t/w, w = fl(1 + t).
+  //
+  // Rounding w = fl(1 + t) drops the low bits of t: ln(w) alone is off by up to 6e-8 absolute,
+  // which for z below about -7 (softplus t-sized) is 1e-4 relative at z = -10 and all of it
+  // below z = -16.6 (w = 1). Both the gate (whose exponent is softplus * rate, so the error
+  // grows with the rate) and d gate / d rate = -gate * softplus need softplus to relative
+  // accuracy there. The dropped part is recovered exactly (Fast2Sum: e = t - (w - 1), both
+  // subtractions exact for t in [0, 1]) and ln(1 + t) = ln(w) + ln(1 + e/w) = ln(w) + e up to
+  // e * t / w < 2^-24 t, below fp32 resolution: the log1p correction for three VALU
+  // instructions and no further transcendental one (4 in all, 3 where only the gate is used).
   __device__ static __forceinline__ void eval(float z, float rate, float& gate, float& dz,
                                               float& dr) {
     constexpr float kLog2e = 1.4426950408889634f;
@@ -179,7 +184,8 @@ struct GateSoftplus {
     // max(z, 0) in one instruction (fmaxf adds a canonicalising one); a NaN z still gives a
     // NaN softplus, through t
     asm("v_max_f32 %0, 0, %1" : "=v"(zpos) : "v"(z));
-    const float sp = fmaf(__builtin_amdgcn_logf(w), kLn2, zpos);
+    const float sum_err = t - (w - 1.0f);  // exact: the part of t that w = fl(1 + t) dropped
+    const float sp = fmaf(__builtin_amdgcn_logf(w), kLn2, zpos + sum_err);
     gate = __builtin_amdgcn_exp2f(-(sp * (rate * kLog2e)));
     const float sig = (z >= 0.0f) ? rw : t * rw;
     dz = -gate * rate * sig;

@@ -54,6 +54,33 @@ def test_backward_matches_oracle(dtype, seqlen):
     assert err <= max(NORM_TOL[dtype], 1e-4), f"grad_rate L{seqlen}: {err:.3e}"
 
 
+@pytest.mark.parametrize("z_mean", [-9.0, -18.0])
+@pytest.mark.parametrize("seqlen", [128, 4096, 65536])
+def test_small_delta_channels_keep_grad_rate_accurate(z_mean, seqlen):
+    """Channels with a small step size (z well below 0, softplus(z) ~ exp(z)): the gate's
+    exponent softplus(z) * rate and d gate / d rate = -gate * softplus(z) need softplus to
+    relative accuracy where 1 + exp(z) rounds to nearly (z = -9) or exactly (z = -18) 1 in
+    fp32. The rates are scaled by exp(-z_mean) so that the gates decay (about 0.99 per step)
+    instead of summing thousands of steps, whose fp32 accumulation alone nears 1e-5. Outputs,
+    grad_rate, grad_z and grad_tokens must meet the fp32 bar against the float64 oracle on
+    short rows, streamed rows and long rows."""
+    gen = torch.Generator().manual_seed(int(-z_mean) * 100 + seqlen)
+    B, D = 2, 6
+    z = torch.randn(B, D, seqlen, generator=gen) + z_mean
+    rate = 0.01 * float(np.exp(-z_mean)) * (0.5 + 1.5 * torch.rand(D, generator=gen))
+    x = 0.1 * torch.randn(B, D, seqlen, generator=gen)
+    go = torch.randn(B, D, seqlen, generator=gen)
+    zd, rd = z.to(DEVICE), rate.to(DEVICE)
+    y = fpscan_amd.scan_forward_softplus(zd, rd, x.to(DEVICE))
+    check(y, oracle.scan_softplus_f64(z, rate, x), torch.float32, f"y z~N({z_mean},1)")
+    gz, gr, gx = fpscan_amd.scan_backward_softplus(zd, rd, y, go.to(DEVICE))
+    gz_ref, gr_ref, gx_ref = oracle.scan_bwd_softplus_f64(z, rate, y.cpu(), go)
+    check(gx, gx_ref, torch.float32, f"grad_tokens z~N({z_mean},1)")
+    check(gz, gz_ref, torch.float32, f"grad_z z~N({z_mean},1)")
+    err = oracle.normwise_error(gr, gr_ref)
+    assert err <= NORM_TOL[torch.float32], f"grad_rate z~N({z_mean},1) L{seqlen}: {err:.3e}"
+
+
 @pytest.mark.parametrize("dtype,L", [(torch.bfloat16, 8192), (torch.float32, 16384)], ids=str)
 def test_short_rows_of_16_to_64_mib_match_oracle(dtype, L):
     """1024 rows of 16 (bf16) or 64 (fp32) sub-chunks, 16-64 MiB per tensor: shapes that
