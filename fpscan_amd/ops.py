@@ -266,7 +266,10 @@ def lookback_overruns(device=None) -> int:
 
 def check_lookback(device=None) -> None:
     """Raises RuntimeError if any look-back wait has given up on ``device`` (whose outputs
-    then hold NaN); a cheap end-of-step check for long runs."""
+    then hold NaN). It synchronises the whole device first (hipDeviceSynchronize) and then
+    copies one counter back, so it drains all queued work: call it at a point where the
+    caller synchronises anyway, such as the end of a training step or of an epoch, not
+    after every scan."""
     n = lookback_overruns(device)
     if n:
         raise RuntimeError(f"fpscan: {n} look-back wait(s) of the tiled scan gave up on this "

@@ -102,8 +102,11 @@ int fpscan_scan_fwd(const void* gates, const void* tokens, void* out,
  * device's scratch and clears it at the start: calls that overlap on one device (other
  * streams, other host threads) race and must be serialised by the caller.
  * No counterpart in the reference (its kernel needs no scratch); for callers that cannot
- * allocate: code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc. */
+ * allocate: tight serving loops and harnesses that forbid hipMalloc. HIP graph capture of
+ * this library's kernels is untested: the one capture that was run (through torch's
+ * torch.cuda.graph, streaming kernels) ended with a host segmentation fault during graph
+ * instantiation, with no cause found, and the torch binding refuses capture since; no
+ * capture through this entry point has been run. */
 int fpscan_scan_fwd_noalloc(const void* gates, const void* tokens, void* out,
                             int64_t batch, int64_t dim, int64_t seqlen,
                             int64_t stride_b, int64_t stride_d,

@@ -120,6 +120,8 @@ SHAPES = [
     (4, 129, 64),     # a last tile of one step (2-byte types)
     (2, 4096, 512),   # 16 chains
     (1, 65536, 64),   # one chain of 512 (1024 in fp32) tiles: the deepest dependency chain
+    (4, 2048, 1024),  # 64 chains: the narrow look-back of depth 5 in every direction and
+                      # type (48-95 chains), consecutive 16-byte pieces of a step per lane
     (8, 2048, 1024),  # 128 chains (look-back depth 3 in the 2-byte forward, else 5; the
                       # 2-byte backward with consecutive lanes on consecutive steps)
 ]
@@ -141,11 +143,13 @@ def test_forward_reverse_backward_match_oracle(lib, tiled, dtype, shape):
     check(gg, gg_ref, dtype, f"tiled {shape} grad_gates")
 
 
-# look-back depths: 8 chains take 5 everywhere; 128 chains 3 in the 2-byte forward and
-# reverse, 5 otherwise; 256 chains 3 in every forward and reverse; the backward always 5.
-# Lane orders: the 2-byte backward puts consecutive lanes on consecutive steps from 96
-# chains (128 and 256 here), every other kernel on consecutive 16-byte pieces of a step.
-DEPTH_SHAPES = [(2, 8192, 256), (8, 1024, 1024), (16, 512, 1024)]
+# look-back depths: below 48 chains the wide look-back (15 aggregates, one word per wave) in
+# every direction and type (8 chains here); 48-95 chains depth 5 everywhere (64 here); 128
+# chains 3 in the 2-byte forward and reverse, 5 otherwise; 256 chains 3 in every forward and
+# reverse; from 48 chains the backward always 5. Lane orders: the 2-byte backward puts
+# consecutive lanes on consecutive steps from 96 chains (128 and 256 here), every other kernel
+# on consecutive 16-byte pieces of a step.
+DEPTH_SHAPES = [(2, 8192, 256), (4, 1024, 1024), (8, 1024, 1024), (16, 512, 1024)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)

@@ -140,6 +140,65 @@ def test_no_less_accurate_than_reference_kernel(seqlen, reverse):
     assert ours <= 4 * theirs + 1e-7, f"ours {ours:.2e} vs reference kernel {theirs:.2e}"
 
 
+# Relative size of one unit in the last place at the top of a binade, 2^-(p-1) for p
+# significand bits: the largest normwise difference two correctly rounded results of nearly
+# equal fp32 values can show.
+ULP_REL = {torch.float32: 2.0 ** -23, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+
+
+def _refkernel_scan(gates, tokens, reverse):
+    """The reference kernel's arithmetic (fp32 accumulation in its combine order,
+    full_scan.cu:77-176) rounded once to the tensors' dtype (conversion.h:7-13)."""
+    return torch.from_numpy(oracle.refkernel_f32(gates, tokens, reverse)).to(gates.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("seqlen", [32, 64, 1024, 8192, 65536])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_half_types_agree_with_reference_kernel(dtype, seqlen, reverse):
+    """fp16/bf16 forward and reverse against the reference kernel's own result: fp32
+    accumulation, then one round-to-nearest-even to the input dtype. The two fp32 results
+    differ only in combine order, so after rounding they agree bit for bit almost everywhere
+    and by one unit in the last place elsewhere; and ours is no less accurate against the
+    float64 recurrence."""
+    g, x = make_inputs(2, 8, seqlen, dtype, seed=seqlen + 11)
+    out = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE), reverse=reverse).cpu()
+    ref_kernel = _refkernel_scan(g, x, reverse)
+    exact = oracle.scan_f64(g, x, reverse)
+    same = (out.view(torch.int16) == ref_kernel.view(torch.int16)).double().mean().item()
+    assert same >= 0.995, f"only {same:.4%} of the outputs equal the reference kernel's bits"
+    assert oracle.normwise_error(out, ref_kernel) <= ULP_REL[dtype]
+    ours = oracle.normwise_error(out, exact)
+    theirs = oracle.normwise_error(ref_kernel, exact)
+    assert ours <= 1.25 * theirs + 1e-7, f"ours {ours:.2e} vs reference kernel {theirs:.2e}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("seqlen", [32, 1024, 8192, 65536])
+def test_backward_agrees_with_reference_composition(dtype, seqlen):
+    """The fused backward against the reference's own backward on the same saved output:
+    PScan.backward's composition (fpscan/ops.py:69-83) -- shifted gates, the reference kernel's
+    reverse scan rounded to the dtype, then grad_gates = out[t-1] * grad_tokens in the dtype's
+    arithmetic (grad_tokens rounded before the product). The fused kernel keeps grad_tokens in
+    fp32 for the product, so grad_gates may differ by one more rounding; both gradients must
+    stay within that and be no less accurate against the float64 adjoint."""
+    g, x = make_inputs(2, 8, seqlen, dtype, seed=seqlen + 21)
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(seqlen)).to(dtype)
+    y = fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE))
+    gg, gx = fpscan_amd.scan_backward(g.to(DEVICE), y, go.to(DEVICE))
+    gg, gx, y = gg.cpu(), gx.cpu(), y.cpu()
+    gg_ref, gx_ref = oracle.pscan_backward_composed(g, y, go, _refkernel_scan)
+    gg64, gx64 = oracle.scan_bwd_f64(g, y, go)
+    tol = max(ULP_REL[dtype], 1e-5)
+    assert oracle.normwise_error(gx, gx_ref) <= tol, "grad_tokens vs the reference composition"
+    assert oracle.normwise_error(gg, gg_ref) <= 2 * tol, "grad_gates vs the reference composition"
+    for name, ours, theirs in (("grad_tokens", gx, gx_ref), ("grad_gates", gg, gg_ref)):
+        want = gx64 if name == "grad_tokens" else gg64
+        e_ours, e_ref = oracle.normwise_error(ours, want), oracle.normwise_error(theirs, want)
+        bound = (4 * e_ref + 1e-7) if dtype == torch.float32 else (1.25 * e_ref + 1e-7)
+        assert e_ours <= bound, f"{name}: ours {e_ours:.2e} vs reference composition {e_ref:.2e}"
+
+
 # ------------------------------------------------------------------ edge cases
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("seqlen", [32, 64, 128, 256, 512, 4096, 65536])
@@ -721,3 +780,47 @@ def test_padded_strides_through_the_c_abi(dtype, L, tiled):
     mask.as_strided((B, D, L), (sb, sd, 1)).fill_(False)
     for buf in (outb, ggb, gxb):
         assert (buf.cpu()[mask] == -3.0).all(), "padding was written"
+
+
+# ------------------------------------------------------------------ HIP graph capture
+# Kept skipped: its one run (the streaming case) ended with a host segmentation fault inside
+# torch.cuda.graph's capture_end (graph instantiation), with a cause not identified. The
+# torch binding now refuses capture before any launch (test_robustness_gpu.py checks that),
+# so this test would fail at the refusal until capture is supported again.
+@pytest.mark.skip(reason="the host process ended with a segmentation fault inside "
+                         "torch.cuda.graph's capture_end on the first (streaming) case; the "
+                         "cause is not identified, so the case stays off the GPU and the "
+                         "binding refuses capture")
+@pytest.mark.parametrize("shape", [(2, 4, 1024), (8, 1024, 65536)], ids=["stream", "tiled"])
+def test_graph_capture_replays_match_eager(shape):
+    """pscan forward + backward captured in a HIP graph (the tiled path's status clear is a
+    kernel, its workspace comes from the graph's pool) and replayed several times with eager
+    work in between; every replay must equal the eager result bit for bit."""
+    import bench
+
+    dtype = torch.bfloat16
+    g, x, go = bench.make_inputs(*shape, dtype, "mamba", seed=12, device=DEVICE)
+    gr = g.clone().requires_grad_()
+    xr = x.clone().requires_grad_()
+
+    def step():
+        y = fpscan_amd.pscan(gr, xr)
+        gg, gx = torch.autograd.grad(y, (gr, xr), go)
+        return y, gg, gx
+
+    want = [t.clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = step()
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert bits_equal(a, b), f"replay {i} differs"
+        fpscan_amd.scan_forward(g, x)  # eager work between replays
+        torch.cuda.synchronize()
