@@ -19,7 +19,10 @@ inputs, on the host cores.
 
 Beside the headline, the default line also carries ``rows_f``: the fused softplus-gate scan,
 the channel-last scan and ``dimwise_forward`` at the same shape in bf16 (``--no-rows`` skips
-them).
+them); ``share_b1``: one GPU's share when the batch is split over eight (B1 D1024 L65536, bf16
+and fp32, forward and backward, with a roofline block); ``c2``: the reference's published
+benchmark (fp32 B2 D256, seqlen 32..65536, forward and reverse) beside the reference's own
+p50s; ``c3`` and ``c5``: BASELINE configs 3 and 5 (``--no-configs`` skips these four).
 
 Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen sweep, forward
 and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant). Multi-GPU runs are not part
@@ -405,6 +408,153 @@ def rows_f_summary(iters):
     return out
 
 
+# The reference's published table (README.md:47-60; eval/benchmark.py:132-217): fp32 B2 D256
+# forward scan_forward on an NVIDIA GeForce RTX 4060 Laptop GPU, p50 ms over 100 iterations.
+REF_C2_P50_MS = {32: 0.0074, 64: 0.0079, 128: 0.0073, 256: 0.0081, 512: 0.0075, 1024: 0.0092,
+                 2048: 0.0133, 4096: 0.0328, 8192: 0.2008, 16384: 0.4362, 32768: 0.8612,
+                 65536: 1.7050}
+
+
+def _timed_entry(fn, nbytes, iters, warm=WARM_CALLS):
+    """p50/p90 (ms) over `iters` event-timed calls after `warm` untimed ones, the mean, and
+    GB/s and fraction of peak at the p50."""
+    t = time_each(fn, warm, iters)
+    p50 = percentile(t, 0.5)
+    gbps = nbytes / (p50 / 1e3) / 1e9
+    return {"p50_ms": round(p50, 5), "p90_ms": round(percentile(t, 0.9), 5),
+            "avg_ms": round(statistics.mean(t), 5), "gbps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
+def share_summary(iters):
+    """One GPU's share of the headline when its batch is split over eight GPUs: B1 D1024
+    L65536 (1024 rows of 65536, the few-rows regime the reference handles with one block per
+    row, full_scan.cu:77-80, 190), in bf16 and fp32. Forward and fused backward kernels alone,
+    each on the path the library picks for the size, with a roofline block for the backward
+    (the larger kernel): 5 N s bytes over its mean event-timed duration."""
+    import fpscan_amd
+
+    B, D, L = 1, 1024, 65536
+    ext = fpscan_amd.ops._load_extension()
+    res = {"shape": f"B{B} D{D} L{L}", "iters": iters}
+    for dtype in (torch.bfloat16, torch.float32):
+        s = torch.empty((), dtype=dtype).element_size()
+        N = B * D * L
+        gates, tokens, grad_out = make_inputs(B, D, L, dtype, "mamba", seed=4)
+        out = torch.empty_like(tokens)
+        y = fpscan_amd.scan_forward(gates, tokens)
+        gg, gx = torch.empty_like(gates), torch.empty_like(gates)
+        dcode = {torch.float32: 0, torch.bfloat16: 2}[dtype]
+        paths = {op: ("scan_tiles" if ext.workspace_bytes(B, D, L, dcode, k) > 0
+                      else "scan_long_rows") for k, op in ((0, "fwd"), (1, "bwd"))}
+        fwd = _timed_entry(lambda: fpscan_amd.scan_forward(gates, tokens, False, out), 3 * N * s,
+                           iters)
+        bwd = _timed_entry(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx),
+                           5 * N * s, iters)
+        achieved = 5 * N * s / (bwd["avg_ms"] / 1e3) / 1e9
+        traffic, src = load_traffic("share_b1", SHORT[dtype])
+        res[SHORT[dtype]] = {
+            "paths": paths, "fwd": fwd, "bwd": bwd,
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                         "traffic": traffic, "kernel": f"{paths['bwd']}<bwd>",
+                         "algorithmic_bytes_per_launch": 5 * N * s, "traffic_source": src},
+        }
+        del gates, tokens, grad_out, out, y, gg, gx
+    return res
+
+
+def c2_summary(iters, warmup=10):
+    """Config 2, the reference's only published benchmark: fp32 B2 D256 scan_forward over
+    seqlen 32..65536 with eval/benchmark.py's inputs and call (a fresh output per call), warmup
+    10 and p50/p90 over `iters`, forward and reverse. Each forward point carries the reference's
+    published p50 (README.md:47-60, an RTX 4060 Laptop GPU) and the ratio to it."""
+    import fpscan_amd
+
+    rows = []
+    for L in C2_SEQLENS:
+        gates, tokens, _ = make_inputs(2, 256, L, torch.float32, "uniform", seed=L, grad=False)
+        nbytes = 3 * 2 * 256 * L * 4
+        row = {"seqlen": L}
+        for name, rev in (("fwd", False), ("rev", True)):
+            t = time_each(lambda: fpscan_amd.scan_forward(gates, tokens, rev), warmup, iters)
+            p50 = percentile(t, 0.5)
+            row[name] = {"p50_ms": round(p50, 5), "p90_ms": round(percentile(t, 0.9), 5),
+                         "gbps": round(nbytes / (p50 / 1e3) / 1e9, 1)}
+        row["ref_fwd_p50_ms"] = REF_C2_P50_MS[L]
+        row["speedup_vs_ref"] = round(REF_C2_P50_MS[L] / row["fwd"]["p50_ms"], 2)
+        rows.append(row)
+        del gates, tokens
+    return {"shape": "fp32 B2 D256", "iters": iters, "warmup": warmup,
+            "ref_source": "README.md:47-60 (RTX 4060 Laptop GPU, fp32 forward)", "rows": rows}
+
+
+def c3_summary(iters):
+    """Config 3: bf16 and fp16 B4 D512 L8192 (fp32 accumulation), forward, reverse and fused
+    backward kernels alone, and the autograd step (pscan + torch.autograd.grad)."""
+    import fpscan_amd
+
+    B, D, L = WORKLOADS["c3"][:3]
+    N = B * D * L
+    res = {"shape": f"B{B} D{D} L{L}", "iters": iters}
+    for dtype in (torch.bfloat16, torch.float16):
+        s = torch.empty((), dtype=dtype).element_size()
+        gates, tokens, grad_out = make_inputs(B, D, L, dtype, "uniform", seed=1)
+        out = torch.empty_like(tokens)
+        y = fpscan_amd.scan_forward(gates, tokens)
+        gg, gx = torch.empty_like(gates), torch.empty_like(gates)
+        g = gates.clone().requires_grad_()
+        x = tokens.clone().requires_grad_()
+
+        def step():
+            return torch.autograd.grad(fpscan_amd.pscan(g, x), (g, x), grad_out)
+
+        res[SHORT[dtype]] = {
+            "fwd": _timed_entry(lambda: fpscan_amd.scan_forward(gates, tokens, False, out),
+                                3 * N * s, iters),
+            "rev": _timed_entry(lambda: fpscan_amd.scan_forward(gates, tokens, True, out),
+                                3 * N * s, iters),
+            "bwd": _timed_entry(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx),
+                                5 * N * s, iters),
+            "step": _timed_entry(step, 8 * N * s, iters),
+        }
+        del gates, tokens, grad_out, out, y, gg, gx, g, x
+    return res
+
+
+def c5_summary(iters):
+    """Config 5: fp32 B64 D4096 L256 (many short rows), forward, reverse and backward kernels
+    alone, and the same data held as (batch, seqlen, dim): transposed in with .mT.contiguous(),
+    scanned and transposed back (README.md:94-99), timed end to end."""
+    import fpscan_amd
+
+    B, D, L = WORKLOADS["c5"][:3]
+    N = B * D * L
+    s = 4
+    gates, tokens, grad_out = make_inputs(B, D, L, torch.float32, "sigmoid", seed=1)
+    out = torch.empty_like(tokens)
+    y = fpscan_amd.scan_forward(gates, tokens)
+    gg, gx = torch.empty_like(gates), torch.empty_like(gates)
+    res = {"shape": f"B{B} D{D} L{L} f32", "iters": iters,
+           "fwd": _timed_entry(lambda: fpscan_amd.scan_forward(gates, tokens, False, out),
+                               3 * N * s, iters),
+           "rev": _timed_entry(lambda: fpscan_amd.scan_forward(gates, tokens, True, out),
+                               3 * N * s, iters),
+           "bwd": _timed_entry(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx),
+                               5 * N * s, iters)}
+    del out, y, gg, gx, grad_out
+    gt, xt = gates.mT.contiguous(), tokens.mT.contiguous()
+    del gates, tokens
+
+    def e2e():
+        return fpscan_amd.scan_forward(gt.mT.contiguous(), xt.mT.contiguous()).mT.contiguous()
+
+    # scan bytes only (3 N s): the three transposes add 6 N s of copies on top
+    res["fwd_via_mT"] = _timed_entry(e2e, 3 * N * s, iters)
+    del gt, xt
+    return res
+
+
 def bench_headline(args):
     B, D, L, dname, dist = WORKLOADS[args.workload]
     dtype = DTYPES[args.dtype or dname]
@@ -440,6 +590,12 @@ def bench_headline(args):
         res["fp32"] = f32
     if args.workload == "c4" and not args.no_rows:
         res["rows_f"] = rows_f_summary(args.steps)
+    if args.workload == "c4" and not args.no_configs:
+        # the one-GPU share of the sharded headline, and BASELINE configs 2, 3 and 5
+        res["share_b1"] = share_summary(args.steps)
+        res["c2"] = c2_summary(args.iters)
+        res["c3"] = c3_summary(args.steps)
+        res["c5"] = c5_summary(args.steps)
     # The CPU baselines run last: 15 s of host work with the GPU idle between the bf16 and
     # fp32 steps was followed, in about one run of four, by a 10 ms stall inside the fp32
     # bracketed loop (none in 4 runs with the baselines last, same box).
@@ -641,6 +797,9 @@ def main():
     ap.add_argument("--no-rows", action="store_true",
                     help="c4: skip the fused-gate, channel-last and dimwise figures reported "
                          "beside the headline")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="c4: skip the B1 share and configs 2, 3 and 5 reported beside the "
+                         "headline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--launch", default=None, help="waves_per_row,ring_depth override")
     ap.add_argument("--tiling", type=int, choices=[0, 1, 2], default=0,
