@@ -25,7 +25,9 @@ benchmark (fp32 B2 D256, seqlen 32..65536, forward and reverse) beside the refer
 p50s; ``c3`` and ``c5``: BASELINE configs 3 and 5 (``--no-configs`` skips these four).
 
 Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen sweep, forward
-and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant). Multi-GPU runs are not part
+and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant), c4cl and c5cl (channel-last),
+dw (dimwise_forward), c4fused (fused softplus gates) and ceiling (the library's copy probes
+with the scans' access patterns, beside the scans). Multi-GPU runs are not part
 of this build: ``--gpus N`` with N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -777,12 +779,76 @@ def bench_dimwise(args):
     return entry
 
 
+PROBE_PATTERNS = {"tiles": 0, "blocks": 1, "rows": 2}  # include/fpscan_probe.h
+
+
+def bench_ceiling(args):
+    """ceiling: the access-pattern ceilings the scans are measured against. The library's
+    bandwidth probes (include/fpscan_probe.h: copy kernels with the scans' access patterns and
+    no scan) move 2 reads + 1 write (the forward's traffic) and 3 reads + 2 writes (the fused
+    backward's) at the headline's per-tensor size (1 GiB: B8 D1024 L65536 bf16) and at the
+    one-GPU share (128 MiB bf16, 256 MiB fp32), beside the forward and backward scans of the
+    same sizes. p50 over --iters calls, GB/s of the bytes each moves."""
+    import ctypes
+
+    import fpscan_amd
+
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(fpscan_amd.__file__), "libfpscan_hip.so"))
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_probe_copy.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, i64, i64,
+                                      vp, ctypes.c_size_t, vp]
+    lib.fpscan_probe_copy.restype = ctypes.c_int
+    lib.fpscan_probe_scratch_bytes.restype = ctypes.c_size_t
+    scratch_bytes = lib.fpscan_probe_scratch_bytes()
+    scratch = torch.empty(scratch_bytes, dtype=torch.uint8, device="cuda")
+    cases = [("headline B8 D1024 L65536 bf16", 8, torch.bfloat16),
+             ("share B1 D1024 L65536 bf16", 1, torch.bfloat16),
+             ("share B1 D1024 L65536 f32", 1, torch.float32)]
+    res = {"workload": "ceiling: access-pattern copy probes beside the scans", "iters": args.iters,
+           "cases": []}
+    for name, B, dtype in cases:
+        D, L = 1024, 65536
+        s = torch.empty((), dtype=dtype).element_size()
+        tensor_bytes = B * D * L * s
+        row_bytes = L * s
+        entry = {"case": name, "tensor_bytes": tensor_bytes, "probes": {}}
+        src = torch.ones(3 * tensor_bytes, dtype=torch.uint8, device="cuda")
+        dst = torch.empty(2 * tensor_bytes, dtype=torch.uint8, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        for pname, pattern in PROBE_PATTERNS.items():
+            for nr, nw in ((2, 1), (3, 2)):
+                def call():
+                    st = lib.fpscan_probe_copy(pattern, nr, nw, src.data_ptr(), dst.data_ptr(),
+                                               tensor_bytes, row_bytes, scratch.data_ptr(),
+                                               scratch_bytes, stream)
+                    if st != 0:
+                        raise RuntimeError(f"fpscan_probe_copy status {st}")
+                e = _timed_entry(call, (nr + nw) * tensor_bytes, args.iters)
+                entry["probes"][f"{pname}_{nr}r{nw}w"] = {"p50_ms": e["p50_ms"], "gbps": e["gbps"],
+                                                          "hbm_frac": e["hbm_frac"]}
+        del src, dst
+        gates, tokens, grad_out = make_inputs(B, D, L, dtype, "mamba", seed=5)
+        out = torch.empty_like(tokens)
+        y = fpscan_amd.scan_forward(gates, tokens)
+        gg, gx = torch.empty_like(gates), torch.empty_like(gates)
+        fwd = _timed_entry(lambda: fpscan_amd.scan_forward(gates, tokens, False, out),
+                           3 * tensor_bytes, args.iters)
+        bwd = _timed_entry(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx),
+                           5 * tensor_bytes, args.iters)
+        entry["scan"] = {"fwd": {k: fwd[k] for k in ("p50_ms", "gbps", "hbm_frac")},
+                         "bwd": {k: bwd[k] for k in ("p50_ms", "gbps", "hbm_frac")}}
+        del gates, tokens, grad_out, out, y, gg, gx
+        print(json.dumps(entry), flush=True)
+        res["cases"].append(entry)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw", "c4fused"])
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw", "c4fused", "ceiling"])
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -843,6 +909,8 @@ def main():
         res = bench_dimwise(args)
     elif args.workload == "c4fused":
         res = bench_fused(args)
+    elif args.workload == "ceiling":
+        res = bench_ceiling(args)
     else:
         res = bench_shape(args)
     print(json.dumps(res), flush=True)

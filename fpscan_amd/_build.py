@@ -53,7 +53,7 @@ def _atomic_out(path):
     return path + ".tmp%d" % os.getpid()
 
 
-HIP_SOURCES = ("fpscan_scan.hip", "fpscan_scan_cl.hip", "fpscan_dimwise.hip")
+HIP_SOURCES = ("fpscan_scan.hip", "fpscan_scan_cl.hip", "fpscan_dimwise.hip", "fpscan_probe.hip")
 
 
 def build_hip_library() -> str:

@@ -1,0 +1,222 @@
+// Bandwidth probes: copy kernels that move the same bytes in the same order as this library's
+// scan kernels, without the scan. Each output tensor is a sum of the input tensors (so every
+// load is consumed) and every access is a 16-byte nontemporal one, as in the scan kernels.
+// What one of them reaches on a device is the ceiling of that access pattern there; bench.py
+// (--workload ceiling) times them beside the scans. No counterpart in the reference.
+//
+// Patterns (FPSCAN_PROBE_*, include/fpscan_probe.h):
+//   TILES   16 KiB tiles of each tensor claimed in order from 8 counters, one per contiguous
+//           eighth of the tiles, by a persistent grid of 1024-thread workgroups (the claim
+//           scheme of the tiled scans, scan_common.h): two tiles in flight per workgroup and
+//           the next claim issued before the current tile's stores.
+//   BLOCKS  one 64-thread workgroup per 2 KiB of each tensor, dispatched in memory order
+//           (the pattern of the row scan on rows of one sub-chunk, one wave per row).
+//   ROWS    one 1024-thread workgroup per row of `row_bytes`, walked in 16 KiB rounds with four
+//           rounds in flight (the pattern of the row-streaming scan with 16 waves per row).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fpscan_probe.h"
+#include "scan_common.h"
+
+namespace {
+
+constexpr int kTileBytes = 16 << 10;  // 1024 lanes x 16 bytes
+
+template <int NR, int NW>
+__device__ __forceinline__ void combine_store(const u32x4 (&v)[NR], const Rsrc (&out)[NW],
+                                              uint32_t off) {
+#pragma unroll
+  for (int o = 0; o < NW; ++o) {
+    u32x4 s = v[0];
+#pragma unroll
+    for (int i = 1; i < NR; ++i) s += v[i] * (unsigned)(o + 1);
+    bst16(out[o], off, s);
+  }
+}
+
+template <int NR, int NW>
+__global__ void __launch_bounds__(1024)
+probe_tiles(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes,
+            uint64_t* __restrict__ status, int64_t ntiles) {
+  const bool leader = threadIdx.x == 0;
+  const uint32_t lane_off = threadIdx.x * 16u;
+  const Rsrc st = __builtin_amdgcn_make_buffer_rsrc(
+      status, (short)0, (int)(kStatusExtraWords * sizeof(uint64_t)), kRsrcWord3);
+  // the status buffer holds no tile words here: the counters start at word kCounterStride
+  Claims<RowGroups> claims{(uint32_t)(kCounterStride * sizeof(uint64_t)),
+                           reinterpret_cast<const uint32_t*>(status + kCounterStride),
+                           RowGroups{ntiles, 0}, (int)(blockIdx.x % kClaimGroups)};
+  const int64_t kBubble = ntiles, kDone = ntiles + 1;
+  __shared__ int64_t next_tile;
+
+  auto tile_rsrc = [&](const char* base, int64_t t) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + t * kTileBytes, (short)0,
+                                             kTileBytes, kRsrcWord3);
+  };
+  auto load = [&](int64_t t, u32x4 (&v)[NR]) {
+    const int64_t tt = t < ntiles ? t : 0;
+    const uint32_t off = t < ntiles ? lane_off : kNoOffset;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) v[i] = bld16(tile_rsrc(src + i * tensor_bytes, tt), off);
+  };
+
+  // the claim for the tile after the next one, made by the leader (and waited for) while the
+  // other waves store the current tile
+  // LDS-only barriers (scan_common.h): __syncthreads would also wait for every load in flight
+  auto claim_after = [&](int64_t known) {
+    lds_barrier();
+    if (leader) next_tile = known < ntiles ? claims.next_now(st, kBubble, kDone) : kDone;
+  };
+  auto store = [&](int64_t t, const u32x4 (&v)[NR]) {
+    Rsrc out[NW];
+#pragma unroll
+    for (int o = 0; o < NW; ++o) out[o] = tile_rsrc(dst + o * tensor_bytes, t);
+    combine_store<NR, NW>(v, out, lane_off);
+  };
+  auto claimed = [&]() {
+    lds_barrier();
+    return (int64_t)__builtin_amdgcn_readfirstlane(next_tile);
+  };
+
+  if (leader) next_tile = claims.next_now(st, kBubble, kDone);
+  int64_t t_a = claimed();
+  claim_after(t_a);
+  int64_t t_b = claimed();
+  // two ring slots, a and b, each holding one tile's loads; while one slot's tile is stored,
+  // the other's loads are in flight
+  u32x4 a[NR], b[NR];
+  load(t_a, a);
+  load(t_b, b);
+  for (;;) {
+    if (t_a >= ntiles) break;
+    claim_after(t_b);
+    store(t_a, a);
+    t_a = claimed();
+    load(t_a, a);
+    if (t_b >= ntiles) break;
+    claim_after(t_a);
+    store(t_b, b);
+    t_b = claimed();
+    load(t_b, b);
+  }
+}
+
+template <int NR, int NW>
+__global__ void __launch_bounds__(64)
+probe_blocks(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes) {
+  constexpr int kBlockBytes = 2 << 10;  // two 1 KiB sub-chunks per wave
+  const int64_t base = (int64_t)blockIdx.x * kBlockBytes;
+  const uint32_t lane_off = threadIdx.x * 16u;
+  u32x4 v[2][NR];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+      v[s][i] = bld16(row_rsrc(src + i * tensor_bytes, base, 1, kBlockBytes),
+                      s * 1024u + lane_off);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    Rsrc out[NW];
+#pragma unroll
+    for (int o = 0; o < NW; ++o) out[o] = row_rsrc(dst + o * tensor_bytes, base, 1, kBlockBytes);
+    combine_store<NR, NW>(v[s], out, s * 1024u + lane_off);
+  }
+}
+
+template <int NR, int NW>
+__global__ void __launch_bounds__(1024)
+probe_rows(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes,
+           int64_t row_bytes) {
+  constexpr int U = 4;
+  const int64_t base = (int64_t)blockIdx.x * row_bytes;
+  const int nrounds = (int)(row_bytes / kTileBytes);
+  const uint32_t lane_off = threadIdx.x * 16u;
+  Rsrc in[NR], out[NW];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) in[i] = row_rsrc(src + i * tensor_bytes, base, 1, (int)row_bytes);
+#pragma unroll
+  for (int o = 0; o < NW; ++o) out[o] = row_rsrc(dst + o * tensor_bytes, base, 1, (int)row_bytes);
+  auto off_of = [&](int r) { return r < nrounds ? (uint32_t)r * kTileBytes + lane_off : kNoOffset; };
+  u32x4 ring[U][NR];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int i = 0; i < NR; ++i) ring[u][i] = bld16(in[i], off_of(u));
+  for (int r0 = 0; r0 < nrounds; r0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = r0 + u;
+      if (r < nrounds) combine_store<NR, NW>(ring[u], out, off_of(r));
+#pragma unroll
+      for (int i = 0; i < NR; ++i) ring[u][i] = bld16(in[i], off_of(r + U));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+template <int NR, int NW>
+int launch_probe(int pattern, const void* src, void* dst, int64_t tensor_bytes, int64_t row_bytes,
+                 void* scratch, hipStream_t stream) {
+  const char* s = static_cast<const char*>(src);
+  char* d = static_cast<char*>(dst);
+  if (pattern == FPSCAN_PROBE_BLOCKS) {
+    const int64_t blocks = tensor_bytes / (2 << 10);
+    hipLaunchKernelGGL((probe_blocks<NR, NW>), dim3((unsigned)blocks), dim3(64), 0, stream, s, d,
+                       tensor_bytes);
+  } else if (pattern == FPSCAN_PROBE_ROWS) {
+    hipLaunchKernelGGL((probe_rows<NR, NW>), dim3((unsigned)(tensor_bytes / row_bytes)),
+                       dim3(1024), 0, stream, s, d, tensor_bytes, row_bytes);
+  } else {
+    uint64_t* status = static_cast<uint64_t*>(scratch);
+    int64_t zero = 0;
+    hipLaunchKernelGGL(clear_status, dim3(1), dim3(256), 0, stream, status, zero);
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&probe_tiles<NR, NW>), 1024, 0) != hipSuccess ||
+        cus <= 0 || per_cu <= 0)
+      return FPSCAN_PROBE_ERR_DEVICE;
+    const int64_t ntiles = tensor_bytes / kTileBytes;
+    const int64_t grid = (int64_t)cus * per_cu < ntiles ? (int64_t)cus * per_cu : ntiles;
+    hipLaunchKernelGGL((probe_tiles<NR, NW>), dim3((unsigned)grid), dim3(1024), 0, stream, s, d,
+                       tensor_bytes, status, ntiles);
+  }
+  return hipGetLastError() == hipSuccess ? FPSCAN_PROBE_OK : FPSCAN_PROBE_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fpscan_probe_scratch_bytes(void) { return kStatusExtraWords * sizeof(uint64_t); }
+
+int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void* dst,
+                      int64_t tensor_bytes, int64_t row_bytes, void* scratch,
+                      size_t scratch_bytes, void* stream) {
+  if (pattern != FPSCAN_PROBE_TILES && pattern != FPSCAN_PROBE_BLOCKS &&
+      pattern != FPSCAN_PROBE_ROWS)
+    return FPSCAN_PROBE_ERR_ARG;
+  if (!((nread == 2 && nwrite == 1) || (nread == 3 && nwrite == 2))) return FPSCAN_PROBE_ERR_ARG;
+  if (src == nullptr || dst == nullptr) return FPSCAN_PROBE_ERR_ARG;
+  if ((reinterpret_cast<uintptr_t>(src) & 15u) != 0 || (reinterpret_cast<uintptr_t>(dst) & 15u) != 0)
+    return FPSCAN_PROBE_ERR_ARG;
+  // whole tiles; at most 4 GiB per tensor keeps every grid below 2^32 work-items
+  if (tensor_bytes <= 0 || tensor_bytes % kTileBytes != 0 || tensor_bytes > (int64_t)1 << 32)
+    return FPSCAN_PROBE_ERR_ARG;
+  if (pattern == FPSCAN_PROBE_ROWS &&
+      (row_bytes <= 0 || row_bytes % kTileBytes != 0 || tensor_bytes % row_bytes != 0 ||
+       row_bytes > INT32_MAX))
+    return FPSCAN_PROBE_ERR_ARG;
+  if (pattern == FPSCAN_PROBE_TILES &&
+      (scratch == nullptr || scratch_bytes < fpscan_probe_scratch_bytes() ||
+       (reinterpret_cast<uintptr_t>(scratch) & 7u) != 0 ||
+       tensor_bytes / kTileBytes > (int64_t)UINT32_MAX))
+    return FPSCAN_PROBE_ERR_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return nread == 2 ? launch_probe<2, 1>(pattern, src, dst, tensor_bytes, row_bytes, scratch, s)
+                    : launch_probe<3, 2>(pattern, src, dst, tensor_bytes, row_bytes, scratch, s);
+}
+
+}  // extern "C"

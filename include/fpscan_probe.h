@@ -1,0 +1,50 @@
+/* Bandwidth probes of the fpscan library (libfpscan_hip.so): copy kernels with the access
+ * patterns of the scan kernels and none of their arithmetic, so that the scans can be
+ * measured against what their own memory-access order reaches on the device (bench.py
+ * --workload ceiling). Measurement aids with no counterpart in the reference (its repository
+ * has no bandwidth probe); the scans do not use them. */
+#ifndef FPSCAN_PROBE_H
+#define FPSCAN_PROBE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Access patterns */
+#define FPSCAN_PROBE_TILES 0  /* 16 KiB tiles claimed in order from 8 counters by a persistent
+                                 grid of 1024-thread workgroups, two tiles in flight each (the
+                                 tiled scans' scheme) */
+#define FPSCAN_PROBE_BLOCKS 1 /* one 64-thread workgroup per 2 KiB, dispatched in memory order
+                                 (the row scan on rows of one sub-chunk) */
+#define FPSCAN_PROBE_ROWS 2   /* one 1024-thread workgroup per row of row_bytes, 16 KiB rounds,
+                                 four in flight (the row-streaming scan, 16 waves per row) */
+
+#define FPSCAN_PROBE_OK 0
+#define FPSCAN_PROBE_ERR_ARG 1    /* unknown pattern or read/write count, bad size, alignment,
+                                     or a missing scratch buffer for FPSCAN_PROBE_TILES */
+#define FPSCAN_PROBE_ERR_LAUNCH 2 /* the launch failed */
+#define FPSCAN_PROBE_ERR_DEVICE 3 /* the current device or the kernel's occupancy could not be
+                                     queried */
+
+/* Bytes of device scratch FPSCAN_PROBE_TILES needs for its claim counters (cleared by the
+ * call, on the stream, before the copy). */
+size_t fpscan_probe_scratch_bytes(void);
+
+/* dst[o] = src[0] + (o + 1) * (src[1] + ... ) as 32-bit integer vectors, for nread inputs laid
+ * out back to back at `src` (nread * tensor_bytes bytes) and nwrite outputs back to back at
+ * `dst`; (nread, nwrite) is (2, 1) -- the forward scan's traffic -- or (3, 2) -- the fused
+ * backward's. tensor_bytes: a multiple of 16 KiB, at most 4 GiB; row_bytes (FPSCAN_PROBE_ROWS
+ * only): a multiple of 16 KiB that divides tensor_bytes. Pointers 16-byte aligned. Enqueued on
+ * `stream` (a hipStream_t; NULL for the default stream). */
+int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void* dst,
+                      int64_t tensor_bytes, int64_t row_bytes, void* scratch,
+                      size_t scratch_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FPSCAN_PROBE_H */

@@ -17,10 +17,15 @@ HEADER = os.path.join(ROOT, "include", "fpscan_hip.h")
 LIB = os.path.join(ROOT, "fpscan_amd", "libfpscan_hip.so")
 
 
-def header_functions():
-    text = open(HEADER).read()
+def header_functions(path=HEADER):
+    text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(fpscan_\w+)\s*\(", text, flags=re.M)
+
+
+def all_headers():
+    inc = os.path.join(ROOT, "include")
+    return sorted(os.path.join(inc, f) for f in os.listdir(inc) if f.endswith(".h"))
 
 
 def header_defines():
@@ -59,8 +64,35 @@ def test_header_declares_the_expected_entry_points():
 
 
 def test_library_exports_every_declared_symbol(lib):
-    for name in header_functions():
-        assert hasattr(lib, name), f"{name} declared in fpscan_hip.h but not exported"
+    headers = all_headers()
+    assert HEADER in headers and len(headers) >= 2
+    for path in headers:
+        for name in header_functions(path):
+            assert hasattr(lib, name), f"{name} declared in {os.path.basename(path)} but not exported"
+
+
+def test_probe_rejects_bad_arguments_before_any_launch(lib):
+    """The bandwidth probe (include/fpscan_probe.h) validates its arguments on the host."""
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_probe_copy.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, i64, i64,
+                                      vp, ctypes.c_size_t, vp]
+    lib.fpscan_probe_copy.restype = ctypes.c_int
+    lib.fpscan_probe_scratch_bytes.restype = ctypes.c_size_t
+    assert lib.fpscan_probe_scratch_bytes() == 8 * 16 * 9
+    buf, kib16 = 1 << 20, 16 << 10
+    bad = [
+        (3, 2, 1, buf, buf, kib16, 0, None, 0),        # unknown pattern
+        (1, 2, 2, buf, buf, kib16, 0, None, 0),        # (2, 2) is not a scan's traffic
+        (1, 2, 1, None, buf, kib16, 0, None, 0),       # null source
+        (1, 2, 1, buf + 8, buf, kib16, 0, None, 0),    # misaligned
+        (1, 2, 1, buf, buf, kib16 + 16, 0, None, 0),   # not whole tiles
+        (1, 2, 1, buf, buf, (1 << 32) + kib16, 0, None, 0),  # above 4 GiB
+        (2, 2, 1, buf, buf, 4 * kib16, 3 * kib16, None, 0),  # rows that do not divide
+        (0, 2, 1, buf, buf, kib16, 0, None, 0),        # tiles without scratch
+        (0, 3, 2, buf, buf, kib16, 0, buf, 64),        # scratch too small
+    ]
+    for args in bad:
+        assert lib.fpscan_probe_copy(*args, None) == 1, args
 
 
 def test_abi_version_matches_header(lib):
