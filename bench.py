@@ -779,7 +779,7 @@ def bench_dimwise(args):
     return entry
 
 
-PROBE_PATTERNS = {"tiles": 0, "blocks": 1, "rows": 2}  # include/fpscan_probe.h
+PROBE_PATTERNS = {"tiles": 0, "blocks": 1, "rows": 2, "blocks_lookback": 3}  # fpscan_probe.h
 
 
 def bench_ceiling(args):
@@ -799,8 +799,9 @@ def bench_ceiling(args):
                                       vp, ctypes.c_size_t, vp]
     lib.fpscan_probe_copy.restype = ctypes.c_int
     lib.fpscan_probe_scratch_bytes.restype = ctypes.c_size_t
-    scratch_bytes = lib.fpscan_probe_scratch_bytes()
-    scratch = torch.empty(scratch_bytes, dtype=torch.uint8, device="cuda")
+    lib.fpscan_probe_lookback_scratch_bytes.argtypes = [i64]
+    lib.fpscan_probe_lookback_scratch_bytes.restype = ctypes.c_size_t
+    import fpscan_amd.ops as ops
     cases = [("headline B8 D1024 L65536 bf16", 8, torch.bfloat16),
              ("share B1 D1024 L65536 bf16", 1, torch.bfloat16),
              ("share B1 D1024 L65536 f32", 1, torch.float32)]
@@ -816,6 +817,9 @@ def bench_ceiling(args):
         dst = torch.empty(2 * tensor_bytes, dtype=torch.uint8, device="cuda")
         stream = torch.cuda.current_stream().cuda_stream
         for pname, pattern in PROBE_PATTERNS.items():
+            scratch_bytes = (lib.fpscan_probe_lookback_scratch_bytes(tensor_bytes) if pname ==
+                             "blocks_lookback" else lib.fpscan_probe_scratch_bytes())
+            scratch = torch.zeros(scratch_bytes, dtype=torch.uint8, device="cuda")
             for nr, nw in ((2, 1), (3, 2)):
                 def call():
                     st = lib.fpscan_probe_copy(pattern, nr, nw, src.data_ptr(), dst.data_ptr(),
@@ -823,9 +827,18 @@ def bench_ceiling(args):
                                                scratch_bytes, stream)
                     if st != 0:
                         raise RuntimeError(f"fpscan_probe_copy status {st}")
+                if pname == "blocks_lookback":
+                    scratch.zero_()
                 e = _timed_entry(call, (nr + nw) * tensor_bytes, args.iters)
-                entry["probes"][f"{pname}_{nr}r{nw}w"] = {"p50_ms": e["p50_ms"], "gbps": e["gbps"],
-                                                          "hbm_frac": e["hbm_frac"]}
+                probe = {"p50_ms": e["p50_ms"], "gbps": e["gbps"], "hbm_frac": e["hbm_frac"]}
+                if pname == "blocks_lookback":
+                    polled, gave_up = scratch[:8].view(torch.int32).tolist()
+                    calls = WARM_CALLS + args.iters
+                    probe["tiles_polling_per_call"] = round(polled / calls, 1)
+                    probe["tiles_per_call"] = tensor_bytes // (16 << 10)
+                    probe["waits_given_up"] = gave_up
+                entry["probes"][f"{pname}_{nr}r{nw}w"] = probe
+            del scratch
         del src, dst
         gates, tokens, grad_out = make_inputs(B, D, L, dtype, "mamba", seed=5)
         out = torch.empty_like(tokens)
@@ -837,6 +850,19 @@ def bench_ceiling(args):
                            5 * tensor_bytes, args.iters)
         entry["scan"] = {"fwd": {k: fwd[k] for k in ("p50_ms", "gbps", "hbm_frac")},
                          "bwd": {k: bwd[k] for k in ("p50_ms", "gbps", "hbm_frac")}}
+        if B == 1:
+            # the one-GPU share on each path forced: rows streamed (1) and tiles (2)
+            for mode, label in ((1, "scan_streaming"), (2, "scan_tiled")):
+                ops.set_tiling(mode)
+                try:
+                    f = _timed_entry(lambda: fpscan_amd.scan_forward(gates, tokens, False, out),
+                                     3 * tensor_bytes, args.iters)
+                    b = _timed_entry(lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx),
+                                     5 * tensor_bytes, args.iters)
+                finally:
+                    ops.set_tiling(0)
+                entry[label] = {"fwd": {k: f[k] for k in ("p50_ms", "gbps", "hbm_frac")},
+                                "bwd": {k: b[k] for k in ("p50_ms", "gbps", "hbm_frac")}}
         del gates, tokens, grad_out, out, y, gg, gx
         print(json.dumps(entry), flush=True)
         res["cases"].append(entry)

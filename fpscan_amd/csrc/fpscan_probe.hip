@@ -13,8 +13,13 @@
 //           (the pattern of the row scan on rows of one sub-chunk, one wave per row).
 //   ROWS    one 1024-thread workgroup per row of `row_bytes`, walked in 16 KiB rounds with four
 //           rounds in flight (the pattern of the row-streaming scan with 16 waves per row).
+//   BLOCKS_LOOKBACK  256-thread blocks of 16 KiB tiles in memory order, each waiting before its
+//           stores until every earlier tile of its row has loaded its data: the wait a
+//           single-pass scan in memory order needs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <atomic>
 
 #include "fpscan_probe.h"
 #include "scan_common.h"
@@ -124,6 +129,74 @@ probe_blocks(const char* __restrict__ src, char* __restrict__ dst, int64_t tenso
   }
 }
 
+// Memory-order blocks with the wait a single-pass scan in that order needs: 256-thread
+// blocks, each one 16 KiB tile of every tensor (four 1 KiB sub-chunks per wave), dispatched in
+// memory order. Once all four waves hold their data, wave 0 publishes one word for the tile
+// and waits until every earlier tile of its row (a row = row_bytes of each tensor, at most 64
+// tiles looked at) has published; then the block stores. Words carry the call's epoch, so the
+// scratch needs no clear between calls. The wait is bounded (kSpinLimit polls); the number of
+// tiles that had to poll and of waits that gave up are counted in the scratch's first words.
+constexpr int kLookbackTileBytes = 16 << 10;
+
+template <int NR, int NW>
+__global__ void __launch_bounds__(256)
+probe_blocks_lookback(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes,
+                      int row_tiles, uint32_t* __restrict__ words, uint32_t epoch) {
+  constexpr int kSubs = 4;
+  const int64_t tile = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t base = tile * kLookbackTileBytes + (int64_t)w * (kSubs << 10);
+  const uint32_t lane_off = lane * 16u;
+  u32x4 v[kSubs][NR];
+#pragma unroll
+  for (int s = 0; s < kSubs; ++s)
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+      v[s][i] = bld16(row_rsrc(src + i * tensor_bytes, base, 1, kSubs << 10), s * 1024u + lane_off);
+  // every wave's loads have arrived once their data is used; then the tile is complete
+  __shared__ uint32_t part[4];
+  uint32_t acc = 0;
+#pragma unroll
+  for (int s = 0; s < kSubs; ++s)
+#pragma unroll
+    for (int i = 0; i < NR; ++i) acc ^= v[s][i].x;
+  if (lane == 0) part[w] = acc;
+  lds_barrier();
+  uint32_t* status = words + 2;  // [0] tiles that polled, [1] waits that gave up
+  if (w == 0) {
+    if (lane == 0)
+      __hip_atomic_store(status + tile, epoch | ((part[0] ^ part[1] ^ part[2] ^ part[3]) & 0u),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int seg = (int)(tile % row_tiles);
+    const bool mine = lane < seg;
+    for (int it = 0;; ++it) {
+      const uint32_t wd = mine ? __hip_atomic_load(status + tile - 1 - lane, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : epoch;
+      if (__builtin_amdgcn_ballot_w64(wd != epoch) == 0) {
+        if (it > 0 && lane == 0)
+          __hip_atomic_fetch_add(words, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      if (it >= kSpinLimit) {
+        if (lane == 0)
+          __hip_atomic_fetch_add(words + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  lds_barrier();
+#pragma unroll
+  for (int s = 0; s < kSubs; ++s) {
+    Rsrc out[NW];
+#pragma unroll
+    for (int o = 0; o < NW; ++o) out[o] = row_rsrc(dst + o * tensor_bytes, base, 1, kSubs << 10);
+    combine_store<NR, NW>(v[s], out, s * 1024u + lane_off);
+  }
+}
+
 template <int NR, int NW>
 __global__ void __launch_bounds__(1024)
 probe_rows(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes,
@@ -164,6 +237,14 @@ int launch_probe(int pattern, const void* src, void* dst, int64_t tensor_bytes, 
     const int64_t blocks = tensor_bytes / (2 << 10);
     hipLaunchKernelGGL((probe_blocks<NR, NW>), dim3((unsigned)blocks), dim3(64), 0, stream, s, d,
                        tensor_bytes);
+  } else if (pattern == FPSCAN_PROBE_BLOCKS_LOOKBACK) {
+    static std::atomic<uint32_t> epoch{0};
+    uint32_t e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+    if (e == 0) e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;  // never 0: cleared
+    const int64_t tiles = tensor_bytes / kLookbackTileBytes;
+    const int row_tiles = (int)(row_bytes / kLookbackTileBytes);
+    hipLaunchKernelGGL((probe_blocks_lookback<NR, NW>), dim3((unsigned)tiles), dim3(256), 0,
+                       stream, s, d, tensor_bytes, row_tiles, static_cast<uint32_t*>(scratch), e);
   } else if (pattern == FPSCAN_PROBE_ROWS) {
     hipLaunchKernelGGL((probe_rows<NR, NW>), dim3((unsigned)(tensor_bytes / row_bytes)),
                        dim3(1024), 0, stream, s, d, tensor_bytes, row_bytes);
@@ -192,11 +273,15 @@ extern "C" {
 
 size_t fpscan_probe_scratch_bytes(void) { return kStatusExtraWords * sizeof(uint64_t); }
 
+size_t fpscan_probe_lookback_scratch_bytes(int64_t tensor_bytes) {
+  return tensor_bytes > 0 ? (size_t)(2 + tensor_bytes / kLookbackTileBytes) * sizeof(uint32_t) : 0;
+}
+
 int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void* dst,
                       int64_t tensor_bytes, int64_t row_bytes, void* scratch,
                       size_t scratch_bytes, void* stream) {
   if (pattern != FPSCAN_PROBE_TILES && pattern != FPSCAN_PROBE_BLOCKS &&
-      pattern != FPSCAN_PROBE_ROWS)
+      pattern != FPSCAN_PROBE_ROWS && pattern != FPSCAN_PROBE_BLOCKS_LOOKBACK)
     return FPSCAN_PROBE_ERR_ARG;
   if (!((nread == 2 && nwrite == 1) || (nread == 3 && nwrite == 2))) return FPSCAN_PROBE_ERR_ARG;
   if (src == nullptr || dst == nullptr) return FPSCAN_PROBE_ERR_ARG;
@@ -208,6 +293,12 @@ int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void*
   if (pattern == FPSCAN_PROBE_ROWS &&
       (row_bytes <= 0 || row_bytes % kTileBytes != 0 || tensor_bytes % row_bytes != 0 ||
        row_bytes > INT32_MAX))
+    return FPSCAN_PROBE_ERR_ARG;
+  if (pattern == FPSCAN_PROBE_BLOCKS_LOOKBACK &&
+      (row_bytes <= 0 || row_bytes % kLookbackTileBytes != 0 || tensor_bytes % row_bytes != 0 ||
+       row_bytes > INT32_MAX || scratch == nullptr ||
+       (reinterpret_cast<uintptr_t>(scratch) & 3u) != 0 ||
+       scratch_bytes < fpscan_probe_lookback_scratch_bytes(tensor_bytes)))
     return FPSCAN_PROBE_ERR_ARG;
   if (pattern == FPSCAN_PROBE_TILES &&
       (scratch == nullptr || scratch_bytes < fpscan_probe_scratch_bytes() ||

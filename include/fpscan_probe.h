@@ -21,6 +21,10 @@ extern "C" {
                                  (the row scan on rows of one sub-chunk) */
 #define FPSCAN_PROBE_ROWS 2   /* one 1024-thread workgroup per row of row_bytes, 16 KiB rounds,
                                  four in flight (the row-streaming scan, 16 waves per row) */
+#define FPSCAN_PROBE_BLOCKS_LOOKBACK 3 /* 256-thread blocks, one 16 KiB tile each, in memory
+                                 order; after its loads a block publishes a word and waits
+                                 (bounded) until every earlier tile of its row of row_bytes
+                                 has published, as a single-pass scan in memory order would */
 
 #define FPSCAN_PROBE_OK 0
 #define FPSCAN_PROBE_ERR_ARG 1    /* unknown pattern or read/write count, bad size, alignment,
@@ -33,12 +37,19 @@ extern "C" {
  * call, on the stream, before the copy). */
 size_t fpscan_probe_scratch_bytes(void);
 
+/* Bytes of device scratch FPSCAN_PROBE_BLOCKS_LOOKBACK needs for tensors of tensor_bytes: two
+ * counters (tiles that had to poll, waits that gave up) and one word per 16 KiB tile. Zero it
+ * once before the first call; the words carry a per-call epoch, so later calls need no clear
+ * and the counters accumulate. */
+size_t fpscan_probe_lookback_scratch_bytes(int64_t tensor_bytes);
+
 /* dst[o] = src[0] + (o + 1) * (src[1] + ... ) as 32-bit integer vectors, for nread inputs laid
  * out back to back at `src` (nread * tensor_bytes bytes) and nwrite outputs back to back at
  * `dst`; (nread, nwrite) is (2, 1) -- the forward scan's traffic -- or (3, 2) -- the fused
- * backward's. tensor_bytes: a multiple of 16 KiB, at most 4 GiB; row_bytes (FPSCAN_PROBE_ROWS
- * only): a multiple of 16 KiB that divides tensor_bytes. Pointers 16-byte aligned. Enqueued on
- * `stream` (a hipStream_t; NULL for the default stream). */
+ * backward's. tensor_bytes: a multiple of 16 KiB, at most 4 GiB; row_bytes: for
+ * FPSCAN_PROBE_ROWS and FPSCAN_PROBE_BLOCKS_LOOKBACK a multiple of 16 KiB that divides
+ * tensor_bytes (ignored otherwise). Pointers 16-byte aligned. Enqueued on `stream` (a
+ * hipStream_t; NULL for the default stream). */
 int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void* dst,
                       int64_t tensor_bytes, int64_t row_bytes, void* scratch,
                       size_t scratch_bytes, void* stream);

@@ -23,10 +23,12 @@ def lib():
                                       vp, ctypes.c_size_t, vp]
     lib.fpscan_probe_copy.restype = ctypes.c_int
     lib.fpscan_probe_scratch_bytes.restype = ctypes.c_size_t
+    lib.fpscan_probe_lookback_scratch_bytes.argtypes = [i64]
+    lib.fpscan_probe_lookback_scratch_bytes.restype = ctypes.c_size_t
     return lib
 
 
-@pytest.mark.parametrize("pattern", [0, 1, 2], ids=["tiles", "blocks", "rows"])
+@pytest.mark.parametrize("pattern", [0, 1, 2, 3], ids=["tiles", "blocks", "rows", "lookback"])
 @pytest.mark.parametrize("nr,nw", [(2, 1), (3, 2)], ids=["2r1w", "3r2w"])
 @pytest.mark.parametrize("tensor_kib,row_kib", [(16, 16), (4096, 128), (49152, 256)])
 def test_probe_moves_every_byte(lib, pattern, nr, nw, tensor_kib, row_kib):
@@ -34,7 +36,9 @@ def test_probe_moves_every_byte(lib, pattern, nr, nw, tensor_kib, row_kib):
     gen = torch.Generator(device="cuda").manual_seed(tensor_kib + 7 * nr)
     src = torch.randint(-1000, 1000, (nr, n), generator=gen, device="cuda", dtype=torch.int32)
     dst = torch.full((nw, n), -7, device="cuda", dtype=torch.int32)
-    scratch = torch.empty(lib.fpscan_probe_scratch_bytes(), dtype=torch.uint8, device="cuda")
+    nbytes = (lib.fpscan_probe_lookback_scratch_bytes(n * 4) if pattern == 3
+              else lib.fpscan_probe_scratch_bytes())
+    scratch = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
     for _ in range(2):  # the tile claims start from a cleared scratch on every call
         st = lib.fpscan_probe_copy(pattern, nr, nw, src.data_ptr(), dst.data_ptr(), n * 4,
                                    row_kib << 10, scratch.data_ptr(), scratch.numel(),
@@ -45,3 +49,5 @@ def test_probe_moves_every_byte(lib, pattern, nr, nw, tensor_kib, row_kib):
             want = src[0] + (o + 1) * src[1:].sum(0, dtype=torch.int32)
             assert torch.equal(dst[o], want), f"output {o}"
         dst.fill_(-7)
+    if pattern == 3:
+        assert scratch[4:8].view(torch.int32).item() == 0, "a look-back wait gave up"
