@@ -155,6 +155,35 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward(const at::Tensor& gates,
   return {grad_gates, grad_tokens};
 }
 
+// ---- pscan as an autograd function in C++: the same computation as the Python PScan
+// (fpscan/ops.py:61-87: the forward saves (gates, out), the backward hands grad_output to the
+// fused backward), with the forward and backward entered from the autograd engine without a
+// Python call each. For calls of tens of microseconds the Python round trips were most of the
+// host time per step.
+struct PScanFunction : public torch::autograd::Function<PScanFunction> {
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& gates,
+                            const at::Tensor& tokens) {
+    at::Tensor out = at::empty_like(tokens);
+    fullscan_forward(gates, tokens, out, false);
+    ctx->save_for_backward({gates, out});
+    return out;
+  }
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const auto saved = ctx->get_saved_variables();
+    const at::Tensor& gates = saved[0];
+    const at::Tensor& out = saved[1];
+    at::Tensor grad_gates = at::empty_like(gates);
+    at::Tensor grad_tokens = at::empty_like(gates);
+    fullscan_backward(gates, out, grads[0].contiguous(), grad_gates, grad_tokens);
+    return {grad_gates, grad_tokens};
+  }
+};
+
+at::Tensor pscan(const at::Tensor& gates, const at::Tensor& tokens) {
+  return PScanFunction::apply(gates, tokens);
+}
+
 // ---- channel-last (batch, seqlen, dim): no reference counterpart (README.md:94-99 has
 // callers transpose instead)
 void check_input_cl(const at::Tensor& t, const char* name) {
@@ -367,6 +396,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "fused backward of the forward scan: (grad_gates, grad_tokens) (HIP, gfx950)",
         pybind11::arg("gates"), pybind11::arg("out"), pybind11::arg("grad_out"),
         pybind11::arg("grad_gates"), pybind11::arg("grad_tokens"));
+  m.def("pscan", &pscan,
+        "differentiable scan: the forward kernel, and the fused backward kernel under autograd",
+        pybind11::arg("gates"), pybind11::arg("tokens"));
   m.def("fullscan_forward_cl", &fullscan_forward_cl,
         "channel-last scan of (batch, seqlen, dim) tensors along seqlen, written into out",
         pybind11::arg("Ax"), pybind11::arg("Bx"), pybind11::arg("out"), pybind11::arg("reverse"));

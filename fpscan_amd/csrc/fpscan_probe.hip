@@ -154,20 +154,14 @@ probe_blocks_lookback(const char* __restrict__ src, char* __restrict__ dst, int6
 #pragma unroll
     for (int i = 0; i < NR; ++i)
       v[s][i] = bld16(row_rsrc(src + i * tensor_bytes, base, 1, kSubs << 10), s * 1024u + lane_off);
-  // every wave's loads have arrived once their data is used; then the tile is complete
-  __shared__ uint32_t part[4];
-  uint32_t acc = 0;
-#pragma unroll
-  for (int s = 0; s < kSubs; ++s)
-#pragma unroll
-    for (int i = 0; i < NR; ++i) acc ^= v[s][i].x;
-  if (lane == 0) part[w] = acc;
+  // each wave waits for all of its loads, then the barrier: past it the whole tile has arrived
+  // (a scan's reduce could start here)
+  __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();
   uint32_t* status = words + 2;  // [0] tiles that polled, [1] waits that gave up
   if (w == 0) {
     if (lane == 0)
-      __hip_atomic_store(status + tile, epoch | ((part[0] ^ part[1] ^ part[2] ^ part[3]) & 0u),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(status + tile, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int seg = (int)(tile % row_tiles);
     const bool mine = lane < seg;
     for (int it = 0;; ++it) {

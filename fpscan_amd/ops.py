@@ -11,7 +11,9 @@ Drop-in for ``fpscan/ops.py`` of saeeddhqan/fpscan:
 * ``PScan.backward`` replaces fpscan/ops.py:69-83 (shifted-gate copy, reverse scan,
   shifted-output copy, product: 7 ATen launches and one scan) with one fused HIP kernel that
   reads gates, out and grad_out once and writes both gradients.
-* ``pscan`` mirrors fpscan/ops.py:86-87.
+* ``pscan`` mirrors fpscan/ops.py:86-87; the autograd function it applies is the C++ twin of
+  ``PScan`` in the extension (same saved tensors, same kernels), which spares the engine a
+  Python call in the forward and in the backward. ``PScan.apply`` keeps working.
 """
 from __future__ import annotations
 
@@ -105,7 +107,10 @@ class PScan(torch.autograd.Function):
 
 
 def pscan(gates: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
-    return PScan.apply(gates, tokens)
+    """Differentiable ``scan_forward(gates, tokens)``: the computation of ``PScan.apply``
+    (fpscan/ops.py:86-87), run by the extension's C++ autograd function so that neither the
+    forward nor the backward makes a Python call (the host time of a short step)."""
+    return _load_extension().pscan(gates, tokens)
 
 
 # ---------------------------------------------------------------------------------------

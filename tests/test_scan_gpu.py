@@ -74,6 +74,30 @@ def test_backward_matches_oracle(dtype, seqlen):
     check(gd.grad, gg_ref, dtype, f"grad_gates {dtype} L{seqlen}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("seqlen", [64, 4096])
+def test_pscan_and_pscan_apply_agree_bit_for_bit(dtype, seqlen):
+    """pscan runs the extension's C++ autograd function, PScan.apply the Python one; both
+    launch the same kernels on the same saved tensors, so outputs and gradients are equal bit
+    for bit, including when only one input requires a gradient."""
+    g, x = make_inputs(3, 5, seqlen, dtype, seed=seqlen + 31)
+    go = torch.randn(g.shape, generator=torch.Generator().manual_seed(3)).to(dtype).to(DEVICE)
+    results = []
+    for fn in (fpscan_amd.pscan, fpscan_amd.PScan.apply):
+        gd = g.to(DEVICE).requires_grad_()
+        xd = x.to(DEVICE).requires_grad_()
+        y = fn(gd, xd)
+        y.backward(go)
+        results.append((y.detach(), gd.grad, xd.grad))
+    for a, b in zip(*results):
+        assert bits_equal(a, b)
+    xd = x.to(DEVICE).requires_grad_()
+    y = fpscan_amd.pscan(g.to(DEVICE), xd)  # gates without a gradient
+    (gx,) = torch.autograd.grad(y, (xd,), go)
+    assert bits_equal(gx, results[0][2])
+    assert not fpscan_amd.pscan(g.to(DEVICE), x.to(DEVICE)).requires_grad
+
+
 def test_non_power_of_two_seqlen_raises():
     g, x = make_inputs(1, 1, 32, torch.float32)
     with pytest.raises(RuntimeError):
