@@ -321,17 +321,26 @@ def measure_training_step(B, D, L, dtype, dist, steps, warmup, workload):
     return res, (gates, tokens, grad_out)
 
 
-# Freed device memory stays in torch's cache for the whole run: returning it to the driver
-# (torch.cuda.empty_cache) between measurements made the next measurement run slow while the
-# driver wiped the released memory in the background (measured: a 10-17 ms stall inside the
-# fp32 step or its backward-kernel timing in half of such runs, and the fused-gate forward
-# that follows the fp32 step 1.8 % slower; none without the release). A default run reserves
-# at most 18 GiB of the 288.
-#
-# Untimed calls before each separately timed kernel or step of the side workloads: the first
-# few dozen milliseconds of GPU work after a pause run a few per cent slow (measured: the
-# channel-last forward's first 20 calls 587 us, then 566-568, the same as its reverse).
+# Each workload after the first starts from an empty allocator cache, as it would in a
+# process of its own: where a workload's tensors land inside segments cached by an earlier
+# workload changes its speed by a few per cent (measured: the fused softplus-gate step 1.503 ms
+# in a fresh process, 1.556 ms after the headline's bf16 and fp32 steps, 1.505-1.510 ms after
+# releasing the cache). The driver wipes released memory in the background and a measurement
+# overlapping that wipe stalls (10-17 ms once in two runs when the release came right before
+# it), so the release is followed by a pause of RELEASE_PAUSE_S, and each measurement then by
+# WARM_CALLS untimed calls: the first few dozen milliseconds of GPU work after a pause run a
+# few per cent slow (the channel-last forward's first 20 calls 587 us, then 566-568).
 WARM_CALLS = 20
+RELEASE_PAUSE_S = 2.0
+
+
+def fresh_allocator():
+    """Returns torch's cached device memory to the driver and waits for it to settle."""
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch.cuda.synchronize()
+    time.sleep(RELEASE_PAUSE_S)
 
 
 def rows_f_summary(iters):
@@ -371,13 +380,16 @@ def rows_f_summary(iters):
                             5 * N * s),
     }
     zr, rr, xr = (t.clone().requires_grad_() for t in (z, rate, x))
+    del z, x, y
+    fresh_allocator()
 
     def step():
         return torch.autograd.grad(fpscan_amd.pscan_softplus(zr, rr, xr), (zr, rr, xr), go)
 
     fused["step"] = timed(step, 8 * N * s)
     out["softplus_fused"] = fused
-    del z, rate, x, go, y, zr, rr, xr
+    del rate, go, zr, rr, xr
+    fresh_allocator()
     # channel-last (batch, seqlen, dim)
     g, x, go = make_inputs(B, L, D, dtype, "mamba", seed=1)
     y = fpscan_amd.scan_forward_channel_last(g, x)
@@ -397,6 +409,7 @@ def rows_f_summary(iters):
                      5 * n1 * s),
     }
     del g, x, go, y, o, gg, gx, g1, x1, go1, y1, o1, gg1, gx1
+    fresh_allocator()
     # dimwise_forward, in place on Bx (each call rescans the previous output: the same work)
     G = fpscan_amd.dimwise_groups(L)
     gen = torch.Generator(device="cuda").manual_seed(2)
@@ -586,18 +599,20 @@ def bench_headline(args):
     if args.workload == "c4" and dtype != torch.float32 and not args.no_fp32:
         # the north star's second dtype, fp32 (the reference's only published dtype): the same
         # step at the same shape, reported beside the headline line's bf16 figures
+        fresh_allocator()
         f32, _ = measure_training_step(B, D, L, torch.float32, dist, args.steps, args.warmup,
                                        args.workload)
         f32["config"] = f"{args.workload}: pscan fwd+bwd B{B} D{D} L{L} f32"
         res["fp32"] = f32
     if args.workload == "c4" and not args.no_rows:
+        fresh_allocator()
         res["rows_f"] = rows_f_summary(args.steps)
     if args.workload == "c4" and not args.no_configs:
         # the one-GPU share of the sharded headline, and BASELINE configs 2, 3 and 5
-        res["share_b1"] = share_summary(args.steps)
-        res["c2"] = c2_summary(args.iters)
-        res["c3"] = c3_summary(args.steps)
-        res["c5"] = c5_summary(args.steps)
+        for key, fn, n in (("share_b1", share_summary, args.steps), ("c2", c2_summary, args.iters),
+                           ("c3", c3_summary, args.steps), ("c5", c5_summary, args.steps)):
+            fresh_allocator()
+            res[key] = fn(n)
     # The CPU baselines run last: 15 s of host work with the GPU idle between the bf16 and
     # fp32 steps was followed, in about one run of four, by a 10 ms stall inside the fp32
     # bracketed loop (none in 4 runs with the baselines last, same box).
