@@ -26,8 +26,8 @@ p50s; ``c3`` and ``c5``: BASELINE configs 3 and 5 (``--no-configs`` skips these 
 
 Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen sweep, forward
 and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant), c4cl and c5cl (channel-last),
-dw (dimwise_forward), c4fused (fused softplus gates) and ceiling (the library's copy probes
-with the scans' access patterns, beside the scans). Multi-GPU runs are not part
+dw (dimwise_forward), c4fused (fused softplus gates), ceiling (the library's copy probes
+with the scans' access patterns, beside the scans) and share (the B1 share object alone). Multi-GPU runs are not part
 of this build: ``--gpus N`` with N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -889,7 +889,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw", "c4fused", "ceiling"])
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw", "c4fused", "ceiling", "share"])
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -952,6 +952,8 @@ def main():
         res = bench_fused(args)
     elif args.workload == "ceiling":
         res = bench_ceiling(args)
+    elif args.workload == "share":
+        res = share_summary(args.steps)
     else:
         res = bench_shape(args)
     print(json.dumps(res), flush=True)
