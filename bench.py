@@ -23,7 +23,7 @@ the channel-last scan and ``dimwise_forward`` at the same shape in bf16 (``--no-
 them); ``share_b1``: one GPU's share when the batch is split over eight (B1 D1024 L65536, bf16
 and fp32, forward and backward, with a roofline block); ``c2``: the reference's published
 benchmark (fp32 B2 D256, seqlen 32..65536, forward and reverse) beside the reference's own
-p50s; ``c3`` and ``c5``: BASELINE configs 3 and 5 (``--no-configs`` skips these four).
+p50s; ``c3`` and ``c5``: configs 3 and 5 of WORKLOADS (``--no-configs`` skips these four).
 
 Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen sweep, forward
 and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant), c4cl and c5cl (channel-last),
@@ -220,7 +220,7 @@ def _cpu_model():
 
 
 def cpu_baseline_c1(warmup=3, iters=20):
-    """BASELINE config 1 on the host cores: the reference's CPU path (Hillis-Steele
+    """Config 1 (fp32 B2 D256 L1024) on the host cores: the reference's CPU path (Hillis-Steele
     ``parallel_scan_torch`` forward, eval/baselines.py:40-61) on fp32 B2 D256 L1024 with the
     reference test's distributions, warmup 3 then p50 of 20 (GB/s at 3*N*4 bytes)."""
     import oracle  # the cpu_baseline leg
@@ -640,7 +640,7 @@ def bench_headline(args):
         fresh_allocator()
         res["rows_f"] = rows_f_summary(args.steps)
     if args.workload == "c4" and not args.no_configs:
-        # the one-GPU share of the sharded headline, and BASELINE configs 2, 3 and 5
+        # the one-GPU share of the sharded headline, and configs 2, 3 and 5
         for key, fn, n in (("share_b1", share_summary, args.steps), ("c2", c2_summary, args.iters),
                            ("c3", c3_summary, args.steps), ("c5", c5_summary, args.steps)):
             fresh_allocator()

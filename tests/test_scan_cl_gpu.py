@@ -12,7 +12,7 @@ takes the tiled look-back, tests/test_scan_cl_tiled_gpu.py, wherever one pass pe
 strips), the one-pass and the segmented (aggregate, carry, apply) paths, the last two forced
 through the C ABI with the tiled look-back switched off (fpscan_set_tiling(1)); ragged and
 non-power-of-two shapes, seqlen 1, partial strips, empty tensors, in-place use, the ignored
-first gate, validation errors, autograd, and the channel-last forms of BASELINE configs 4 and
+first gate, validation errors, autograd, and the channel-last forms of benchmark configs 4 and
 5 at their real shapes.
 """
 import contextlib
@@ -255,7 +255,8 @@ def test_autograd_matches_oracle(dtype):
 
 
 def test_config5_channel_last_b64_l256_d4096():
-    """BASELINE config 5's transposed variant without the transposes."""
+    """Config 5 (fp32 B64 D4096 L256) in its transposed (batch, seqlen, dim) form, without the
+    transposes."""
     import bench
 
     gr, xr, gor = bench.make_inputs(64, 4096, 256, torch.float32, "sigmoid", seed=5,

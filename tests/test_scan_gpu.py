@@ -11,9 +11,9 @@ tolerances (test_fpscan.py:18-22), and adds:
 * bit-exact known answers (tests/golden) and bit-exact size-independent properties at full
   size: reverse == flip(forward(flip)), scaling tokens by 2 scales outputs by exactly 2, the
   fused backward equals a reverse scan of the shifted gates;
-* every configuration of BASELINE.json at its real shape, and the edge cases the reference
-  does not test (ragged row counts, empty tensors, dim > 65535, `out=` and in-place use,
-  first-gate NaN, side streams, every launch shape).
+* every benchmark configuration (bench.py's WORKLOADS, c1-c5) at its real shape, and the edge
+  cases the reference does not test (ragged row counts, empty tensors, dim > 65535, `out=` and
+  in-place use, first-gate NaN, side streams, every launch shape).
 """
 from fractions import Fraction
 
@@ -408,7 +408,7 @@ def test_properties_mid_size(dtype):
     _properties(g.to(DEVICE), x.to(DEVICE), go.to(DEVICE), rows_checked=16)
 
 
-# ------------------------------------------------------------------ BASELINE configs
+# ------------------------------------------------------------------ benchmark configs
 def test_config1_b2_d256_l1024_fp32():
     g, x = make_inputs(2, 256, 1024, torch.float32, seed=0)
     check(fpscan_amd.scan_forward(g.to(DEVICE), x.to(DEVICE)), oracle.scan_f64(g, x),
