@@ -777,11 +777,16 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
   };
   // Steady state: the exit test sits after whole rings. With an exit inside the unrolled
   // body, the compiler's wait counts at the loop head collapse to waiting for every load in
-  // flight.
+  // flight. Only the claim stream ends the loop, never an empty ring: while a workgroup moves
+  // between used-up groups its refills can be bubbles for a whole ring, and the claims it
+  // issued in the last two steps may still hold tiles; leaving then would drop those tiles
+  // (never reduced, published or written), and every later tile of their rows would wait out
+  // the spin limit. Once a claim comes back kDone, the claims still in flight were made to
+  // the same used-up group after it, so they hold no tile.
   for (;;) {
 #pragma unroll
     for (int u = 0; u < N; ++u) step(u);
-    if (!busy() || all_claimed) break;
+    if (all_claimed) break;
   }
   if (!busy()) return;
   // Drain: no tile is claimed any more, so nothing is loaded and waiting for everything in

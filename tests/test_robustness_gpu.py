@@ -244,6 +244,45 @@ def test_hook_off_restores_normal_runs():
     assert not torch.isnan(y).any()
 
 
+# ------------------------------------------------------------------ no tile is ever dropped
+@pytest.mark.parametrize("dtype,op,calls", [(torch.float32, "fwd", 400),
+                                            (torch.bfloat16, "fwd", 200),
+                                            (torch.float32, "bwd", 100)],
+                         ids=["f32-fwd", "bf16-fwd", "f32-bwd"])
+def test_repeated_headline_calls_drop_no_tile(dtype, op, calls):
+    """Hundreds of back-to-back tiled calls at the headline shape (8, 1024, 65536): outputs
+    filled with NaN before each call come back finite every time, no wait gives up, and the
+    last call equals the first bit for bit. A workgroup that left its loop on an empty ring
+    while claims were still in flight dropped the tiles those claims held (their outputs were
+    never written and the later tiles of their rows gave up waiting), a few calls in a
+    hundred; the loop now ends only on the claim stream's end."""
+    g, x, go = bench.make_inputs(8, 1024, 65536, dtype, "mamba", seed=21)
+    y = fpscan_amd.scan_forward(g, x)
+    outs = [torch.empty_like(x)] if op == "fwd" else [torch.empty_like(x), torch.empty_like(x)]
+    nan_seen = torch.zeros((), dtype=torch.bool, device=DEVICE)
+    first = None
+    torch.cuda.synchronize()
+    before = fpscan_amd.lookback_overruns()
+    for i in range(calls):
+        for o in outs:
+            o.fill_(float("nan"))
+        if op == "fwd":
+            fpscan_amd.scan_forward(g, x, False, outs[0])
+        else:
+            fpscan_amd.scan_backward(g, y, go, outs[0], outs[1])
+        for o in outs:
+            nan_seen |= torch.isnan(o).any()
+        if i == 0:
+            first = [o.clone() for o in outs]
+    torch.cuda.synchronize()
+    after = fpscan_amd.lookback_overruns()
+    assert after == before, f"{after - before} look-back waits gave up in {calls} calls"
+    assert not bool(nan_seen), "an output element was left unwritten or poisoned"
+    for a, b in zip(outs, first):
+        assert torch.equal(a.view(torch.int16 if a.element_size() == 2 else torch.int32),
+                           b.view(torch.int16 if b.element_size() == 2 else torch.int32))
+
+
 # ------------------------------------------------------------------ graph capture is refused
 def test_graph_capture_is_refused_before_any_launch():
     hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch has loaded (same SONAME)
