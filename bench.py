@@ -645,9 +645,8 @@ def bench_headline(args):
                            ("c3", c3_summary, args.steps), ("c5", c5_summary, args.steps)):
             fresh_allocator()
             res[key] = fn(n)
-    # The CPU baselines run last: 15 s of host work with the GPU idle between the bf16 and
-    # fp32 steps was followed, in about one run of four, by a 10 ms stall inside the fp32
-    # bracketed loop (none in 4 runs with the baselines last, same box).
+    # The CPU baselines run last, after every GPU measurement, so that 15 s of host work
+    # never sits between two of them.
     if args.no_cpu_baseline:
         res["cpu_baseline"] = None
     else:
@@ -972,6 +971,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    import fpscan_amd
+
+    overruns_before = fpscan_amd.lookback_overruns()
     if args.workload == "c4":
         res = bench_headline(args)
     elif args.workload == "c2":
@@ -988,6 +990,13 @@ def main():
         res = share_summary(args.steps)
     else:
         res = bench_shape(args)
+    # health of the tiled kernels over the whole run: look-back waits that gave up (0 in a
+    # correct run; each one leaves NaN outputs and about 10 ms of waiting in its call)
+    overruns = fpscan_amd.lookback_overruns() - overruns_before
+    if isinstance(res, dict):
+        res["lookback_overruns"] = overruns
+    if overruns:
+        print(f"bench.py: {overruns} look-back waits gave up during the run", file=sys.stderr)
     print(json.dumps(res), flush=True)
 
 
