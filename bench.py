@@ -12,8 +12,9 @@ itemsize (eval/benchmark.py:62-65 counts the forward the same way):
     backward 5*N*s  (read gates, out, grad_out; write grad_gates, grad_tokens)
     step     8*N*s
 ``value`` = step bytes / (bracketed wall time of K steps / K), in GB/s. ``roofline`` is the
-backward kernel (the dominant one), timed alone on the stream it runs on: K back-to-back calls
-inside one HIP event pair, 5*N*s bytes over the mean duration.
+backward kernel (the dominant one), timed alone on the stream it runs on and on the timed
+step's own buffers: K back-to-back calls inside one HIP event pair, 5*N*s bytes over the mean
+duration.
 ``cpu_baseline`` times the reference's CPU path -- Hillis-Steele ``parallel_scan_torch``
 forward plus the PScan.backward composition -- on a bounded sample of rows of the same
 inputs, on the host cores.
@@ -299,21 +300,24 @@ def measure_training_step(B, D, L, dtype, dist, steps, warmup, workload):
         gc.enable()
     ms_per_step = start.elapsed_time(end) / steps
     step_p = time_each(step, 1, steps)
-    del g, x
 
-    # kernels alone
-    out = torch.empty_like(tokens)
-    gg = torch.empty_like(gates)
-    gx = torch.empty_like(gates)
-    fwd = lambda: fpscan_amd.scan_forward(gates, tokens, out=out)  # noqa: E731
+    # Kernels alone, on the timed step's own buffers: its inputs, and the forward output and
+    # the two gradients of one more step (the caching allocator hands every step the same
+    # blocks). The kernels' speed depends on where their tensors sit in HBM by several per
+    # cent (the fused backward at the headline: 842-871 us over six output placements in one
+    # process), so buffers allocated apart from the step would time a different placement.
+    y = fpscan_amd.pscan(g, x)
+    gg, gx = torch.autograd.grad(y, (g, x), grad_out)
+    y = y.detach()
+    gd, xd = g.detach(), x.detach()
+    fwd = lambda: fpscan_amd.scan_forward(gd, xd, out=y)  # noqa: E731
     fwd_t = time_each(fwd, 2, steps)
-    y = fpscan_amd.scan_forward(gates, tokens)
-    bwd = lambda: fpscan_amd.scan_backward(gates, y, grad_out, gg, gx)  # noqa: E731
+    bwd = lambda: fpscan_amd.scan_backward(gd, y, grad_out, gg, gx)  # noqa: E731
     bwd_t = time_each(bwd, 2, steps)
     # the roofline's average launch duration: one event pair over `steps` back-to-back calls
     fwd_avg = time_bracketed(fwd, 2, steps)
     bwd_avg = time_bracketed(bwd, 2, steps)
-    del out, gg, gx, y
+    del y, gg, gx, gd, xd, g, x
     bwd_bytes = 5 * N * s
     achieved = bwd_bytes / (bwd_avg / 1e3) / 1e9
     traffic, traffic_src = load_traffic(workload, SHORT[dtype])
@@ -332,8 +336,9 @@ def measure_training_step(B, D, L, dtype, dist, steps, warmup, workload):
                        "gbps": round(3 * N * s / (fwd_avg / 1e3) / 1e9, 1)},
         "bwd_kernel": {"avg_ms": round(bwd_avg, 5), "p50_ms": round(percentile(bwd_t, 0.5), 5),
                        "gbps": round(achieved, 1)},
-        "kernel_timing": "avg_ms: one event pair over back-to-back calls (the roofline's "
-                         "average launch duration); p50_ms: per-call event pairs",
+        "kernel_timing": "on the timed step's own buffers; avg_ms: one event pair over "
+                         "back-to-back calls (the roofline's average launch duration); "
+                         "p50_ms: per-call event pairs",
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
