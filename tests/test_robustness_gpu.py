@@ -8,6 +8,9 @@
   The affected tiles must come out NaN (never plausible numbers), every other value must equal
   an unhooked run bit for bit, and the per-device counter must report the given-up waits. The
   reference has no cross-workgroup wait (full_scan.cu:77-175 keeps every carry in one block).
+* Long runs: hundreds of back-to-back tiled calls (row and channel-last kernels) at the
+  headline size and the one-GPU share, outputs filled with NaN before each call, so that a tile
+  that is dropped or a wait that gives up in one call in a hundred is seen.
 * HIP graph capture through the torch binding is refused with a RuntimeError before anything
   is launched (the capture is begun and ended with the runtime's own calls, no graph is
   instantiated).
@@ -281,6 +284,38 @@ def test_repeated_headline_calls_drop_no_tile(dtype, op, calls):
     for a, b in zip(outs, first):
         assert torch.equal(a.view(torch.int16 if a.element_size() == 2 else torch.int32),
                            b.view(torch.int16 if b.element_size() == 2 else torch.int32))
+
+
+@pytest.mark.parametrize("batch,op,calls", [(8, "fwd", 100), (1, "fwd", 200), (1, "bwd", 200)],
+                         ids=["b8-fwd", "b1-fwd", "b1-bwd"])
+def test_repeated_channel_last_tiled_calls_drop_no_tile(batch, op, calls):
+    """The channel-last tiled kernel (its own look-back across workgroups) under the same
+    long-run check: (batch, 65536, 1024) bf16, outputs filled with NaN before each call, every
+    output written, no wait given up, the last call equal to the first bit for bit."""
+    g, x, go = bench.make_inputs(batch, 65536, 1024, torch.bfloat16, "mamba", seed=22)
+    y = fpscan_amd.scan_forward_channel_last(g, x)
+    outs = [torch.empty_like(x)] if op == "fwd" else [torch.empty_like(x), torch.empty_like(x)]
+    nan_seen = torch.zeros((), dtype=torch.bool, device=DEVICE)
+    first = None
+    torch.cuda.synchronize()
+    before = fpscan_amd.lookback_overruns()
+    for i in range(calls):
+        for o in outs:
+            o.fill_(float("nan"))
+        if op == "fwd":
+            fpscan_amd.scan_forward_channel_last(g, x, False, outs[0])
+        else:
+            fpscan_amd.scan_backward_channel_last(g, y, go, outs[0], outs[1])
+        for o in outs:
+            nan_seen |= torch.isnan(o).any()
+        if i == 0:
+            first = [o.clone() for o in outs]
+    torch.cuda.synchronize()
+    after = fpscan_amd.lookback_overruns()
+    assert after == before, f"{after - before} look-back waits gave up in {calls} calls"
+    assert not bool(nan_seen), "an output element was left unwritten or poisoned"
+    for a, b in zip(outs, first):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
 # ------------------------------------------------------------------ graph capture is refused
