@@ -596,9 +596,20 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
 
   // Claim results: a tile index, kBubble (no tile this step, more to come) or kDone.
   const int64_t kBubble = ntiles, kDone = ntiles + 1;
+  // First claim group. Forward and reverse: blockIdx % 8, so that under round-robin dispatch
+  // each XCD works through one group and a tile's predecessors were published on its own XCD.
+  // Backward: blockIdx / 8 % 8, every group served by workgroups of all eight XCDs, so that
+  // the groups advance at the XCDs' mean speed and end together instead of waiting for the
+  // slowest XCD's group. A/B on MI355X (same buffers, alternated, median of 7, tiled calls at
+  // D1024 L65536): backward B8 bf16 888.8 -> 881.1 us, fp32 1768.5 -> 1715.1, B4 431.9 ->
+  // 425.8 / 918.1 -> 858.1, B2 bf16 234.1 -> 216.9, B1 fp32 238.3 -> 223.6; the forward
+  // loses with it (B8 fp32 1012.4 -> 1057.6: its shorter steps wait on words published
+  // across the device).
+  const int first_group = kMode == kBwd ? (int)((blockIdx.x / kClaimGroups) % kClaimGroups)
+                                        : (int)(blockIdx.x % kClaimGroups);
   Claims<RowGroups> claims{(uint32_t)((ntiles + kCounterStride) * sizeof(uint64_t)),
                            reinterpret_cast<const uint32_t*>(status + ntiles + kCounterStride),
-                           RowGroups{ntiles >> tpr_log2, tpr_log2}, (int)(blockIdx.x % kClaimGroups)};
+                           RowGroups{ntiles >> tpr_log2, tpr_log2}, first_group};
   // leader: claims in flight. Step u of the unrolled ring issues into pending[u] and resolves
   // pending[(u + D) % N], issued two steps earlier; no copies, which would wait for the atomic.
   Claim pending[N];

@@ -404,8 +404,10 @@ struct RowGroups {
 // Tile claims, made by one lane per workgroup. One counter at one address serialises at the
 // memory side (measured: about 70 claims per microsecond, fewer than a bf16 forward scan
 // finishes tiles), so the tiles are split into kClaimGroups contiguous ranges with a counter
-// each (whole rows, or whole chains of the channel-last scan, per group: `Groups`). A workgroup starts in group blockIdx % kClaimGroups (its XCD under round-robin
-// dispatch) and, when that one is used up, moves to the group with the most tiles left. A
+// each (whole rows, or whole chains of the channel-last scan, per group: `Groups`). A
+// workgroup starts in the group its kernel picks (most: blockIdx % kClaimGroups, its XCD
+// under round-robin dispatch) and, when that one is used up, moves to the group with the most
+// tiles left. A
 // row never spans two groups and tiles of a group are claimed in order, so a tile's
 // predecessors are always claimed before it. Claims are issued two steps before their tile
 // is needed (an atomic at the memory side takes a few microseconds under full streaming
