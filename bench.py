@@ -537,8 +537,17 @@ def c2_summary(iters, warmup=10):
         row["speedup_vs_ref"] = round(REF_C2_P50_MS[L] / row["fwd"]["p50_ms"], 2)
         rows.append(row)
         del gates, tokens
+    # What the same timing reads with no scan: an event pair around a call that launches no
+    # kernel (the output allocation alone), and around torch's own smallest kernel at the
+    # seqlen-32 shape. At short seqlens a scan call costs about what the latter does.
+    x = torch.zeros((2, 256, 32), dtype=torch.float32, device="cuda")
+    alloc = time_each(lambda: torch.empty_like(x), warmup, iters)
+    add = time_each(lambda: x.add_(0.0), warmup, iters)
+    floor = {"alloc_only_p50_ms": round(percentile(alloc, 0.5), 5),
+             "torch_add_p50_ms": round(percentile(add, 0.5), 5)}
     return {"shape": "fp32 B2 D256", "iters": iters, "warmup": warmup,
-            "ref_source": "README.md:47-60 (RTX 4060 Laptop GPU, fp32 forward)", "rows": rows}
+            "ref_source": "README.md:47-60 (RTX 4060 Laptop GPU, fp32 forward)", "rows": rows,
+            "event_floor_l32": floor}
 
 
 def c3_summary(iters):
