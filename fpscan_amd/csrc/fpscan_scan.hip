@@ -901,11 +901,16 @@ constexpr int kTileDefer = 2;
 constexpr int64_t kTiledMinBytes = 512ll << 20;
 // The fused backward moves 5 tensors per tile instead of 3, so the same fixed cost is a smaller
 // share, and the streaming backward slows down on long rows (one workgroup per row streaming
-// 128 KiB or more per tensor). There tiling wins from 256 MiB per tensor: bf16 B2 D1024 L65536
-// 227 us against 241, fp32 B3 D1024 L32768 341 against 363, while on 32-64 KiB rows of the
-// same size streaming still wins by 2-9 %.
+// 64 KiB or more per tensor). There tiling wins from 256 MiB per tensor. Measured on MI355X
+// with the backward's claim groups served by every XCD (same buffers, streaming and tiled
+// forced alternately, median of 5, us): 128 KiB rows bf16 B2 D1024 L65536 216-221 against
+// 238-240, fp32 B2 D1024 L32768 220.5 against 239.0; 64 KiB rows bf16 (4, 1024, 32768)
+// 216.1-216.5 against 229.3-231.0, (8, 512, 32768) 227.8 against 232.7, (2, 2048, 32768)
+// 215.1 against 233.0, fp32 (4, 1024, 16384) and (8, 512, 16384) even (221-222 against
+// 223); 32 KiB rows still stream faster (bf16 (8, 1024, 16384) 219.5 against 228.3, fp32
+// (8, 1024, 8192) 215.9 against 223.9), and at 128 MiB the two paths are within 5 % either way.
 constexpr int64_t kTiledMinBytesBwdLongRows = 256ll << 20;
-constexpr int64_t kLongRowBytes = 128ll << 10;
+constexpr int64_t kLongRowBytes = 64ll << 10;
 // Rows of one tile (16 sub-chunks) stream as 8-wave rows, which keep up with the tiles to
 // about 1 GiB per tensor: at 512 MiB streaming measured 3-8 % faster (bf16 32768 rows of L8192
 // forward / backward 255 / 420 us against 261-278 / 438; fp32 32768 rows of L4096 256 / 428

@@ -123,11 +123,14 @@ def test_workspace_plan(lib):
     assert lib.fpscan_workspace_bytes(2, 256, 1024, 0, 0) == 0
     assert lib.fpscan_workspace_bytes(64, 4096, 256, 0, 0) == 0
     assert lib.fpscan_workspace_bytes(2, 256, 65536, 0, 0) == 0  # 128 MiB per tensor
-    # from 256 MiB per tensor the backward tiles rows of 128 KiB or more; the forward waits
+    # from 256 MiB per tensor the backward tiles rows of 64 KiB or more; the forward waits
     # for 512 MiB, and shorter rows stream in both
     tiles_b2 = 2 * 1024 * (65536 // 512 // 16)
     assert lib.fpscan_workspace_bytes(2, 1024, 65536, 2, 1) == 8 * (tiles_b2 + extra)
     assert lib.fpscan_workspace_bytes(2, 1024, 65536, 2, 0) == 0
+    tiles_64k = 4 * 1024 * (32768 // 512 // 16)  # 64 KiB rows
+    assert lib.fpscan_workspace_bytes(4, 1024, 32768, 2, 1) == 8 * (tiles_64k + extra)
+    assert lib.fpscan_workspace_bytes(4, 1024, 32768, 2, 0) == 0
     assert lib.fpscan_workspace_bytes(8, 1024, 16384, 2, 1) == 0  # 32 KiB rows
     assert lib.fpscan_workspace_bytes(1, 1024, 65536, 2, 1) == 0  # 128 MiB per tensor
     # rows of one tile (16 sub-chunks: bf16 L8192, fp32 L4096) stream up to 1 GiB per tensor

@@ -726,14 +726,15 @@ def test_tiled_and_streaming_paths_agree_and_default_is_tiled_when_large():
     check(tiled.reshape(8192, -1)[rows], oracle.scan_f64(gs, xs), torch.bfloat16, "tiled c4")
 
 
-def test_backward_tiles_long_rows_from_256_mib():
-    """bf16 B2 D1024 L65536 (256 MiB per tensor, 128 KiB rows): the automatic plan tiles the
-    backward but streams the forward. The automatic backward agrees with the streamed one and
-    with the oracle on sampled rows."""
+@pytest.mark.parametrize("B,L", [(2, 65536), (4, 32768)], ids=["rows128k", "rows64k"])
+def test_backward_tiles_long_rows_from_256_mib(B, L):
+    """bf16 (B, 1024, L) at 256 MiB per tensor with rows of 128 KiB and 64 KiB: the automatic
+    plan tiles the backward but streams the forward. The automatic backward agrees with the
+    streamed one and with the oracle on sampled rows."""
     lib = _abi()
-    assert lib.fpscan_workspace_bytes(2, 1024, 65536, 2, 1) > 0
-    assert lib.fpscan_workspace_bytes(2, 1024, 65536, 2, 0) == 0
-    g, x, go = _bench_inputs(2, 1024, 65536, torch.bfloat16, "mamba", seed=8)
+    assert lib.fpscan_workspace_bytes(B, 1024, L, 2, 1) > 0
+    assert lib.fpscan_workspace_bytes(B, 1024, L, 2, 0) == 0
+    g, x, go = _bench_inputs(B, 1024, L, torch.bfloat16, "mamba", seed=8)
     y = fpscan_amd.scan_forward(g, x)
     gg, gx = fpscan_amd.scan_backward(g, y, go)  # automatic: tiled
     try:
@@ -744,12 +745,13 @@ def test_backward_tiles_long_rows_from_256_mib():
     torch.cuda.synchronize()
     assert oracle.normwise_error(gx, gx_s) < 2e-2
     assert oracle.normwise_error(gg, gg_s) < 2e-2
-    rows = torch.linspace(0, 2047, 8).long()
-    gs = g.reshape(2048, -1)[rows].cpu()
-    ys, gos = y.reshape(2048, -1)[rows].cpu(), go.reshape(2048, -1)[rows].cpu()
+    nrows = B * 1024
+    rows = torch.linspace(0, nrows - 1, 8).long()
+    gs = g.reshape(nrows, -1)[rows].cpu()
+    ys, gos = y.reshape(nrows, -1)[rows].cpu(), go.reshape(nrows, -1)[rows].cpu()
     gg_ref, gx_ref = oracle.scan_bwd_f64(gs, ys, gos)
-    check(gx.reshape(2048, -1)[rows], gx_ref, torch.bfloat16, "tiled bwd 256 MiB grad_tokens")
-    check(gg.reshape(2048, -1)[rows], gg_ref, torch.bfloat16, "tiled bwd 256 MiB grad_gates")
+    check(gx.reshape(nrows, -1)[rows], gx_ref, torch.bfloat16, "tiled bwd 256 MiB grad_tokens")
+    check(gg.reshape(nrows, -1)[rows], gg_ref, torch.bfloat16, "tiled bwd 256 MiB grad_gates")
 
 
 # ------------------------------------------------------------------ padded strides (C ABI)
