@@ -135,6 +135,10 @@ __global__ void __launch_bounds__(64 * NW) dimwise_rows(const DwArgs a) {
         float av[V], bv[V];
         E::unpack(ring[u][0], av);
         E::unpack(ring[u][1], bv);
+        // refill this slot with the chunk two ahead now, so its loads overlap this chunk's
+        // scans, selection and barriers
+        ring[u][0] = bld16(ax, chunk_off(c + 2));
+        ring[u][1] = bld16(bx, chunk_off(c + 2));
         if (c == 0 && w == 0 && lane == 0) av[0] = 1.0f;  // the row's first gate is ignored
 
         // local scans: lane aggregate, segmented scan over the group's lanes, then the
@@ -182,9 +186,6 @@ __global__ void __launch_bounds__(64 * NW) dimwise_rows(const DwArgs a) {
 #pragma unroll
         for (int i = 0; i < V; ++i) o[i] = ys[i] + add;
         bst16(bx, chunk_off(c), E::pack(o));
-        // refill this slot with the chunk two ahead
-        ring[u][0] = bld16(ax, chunk_off(c + 2));
-        ring[u][1] = bld16(bx, chunk_off(c + 2));
         __builtin_amdgcn_sched_barrier(0);
       }
     }
