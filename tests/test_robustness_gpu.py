@@ -250,18 +250,20 @@ def test_hook_off_restores_normal_runs():
 # ------------------------------------------------------------------ no tile is ever dropped
 @pytest.mark.parametrize("dtype,op,calls", [(torch.float32, "fwd", 400),
                                             (torch.bfloat16, "fwd", 200),
-                                            (torch.float32, "bwd", 100)],
-                         ids=["f32-fwd", "bf16-fwd", "f32-bwd"])
+                                            (torch.float32, "rev", 200),
+                                            (torch.float32, "bwd", 100),
+                                            (torch.bfloat16, "bwd", 100)],
+                         ids=["f32-fwd", "bf16-fwd", "f32-rev", "f32-bwd", "bf16-bwd"])
 def test_repeated_headline_calls_drop_no_tile(dtype, op, calls):
-    """Hundreds of back-to-back tiled calls at the headline shape (8, 1024, 65536): outputs
-    filled with NaN before each call come back finite every time, no wait gives up, and the
-    last call equals the first bit for bit. A workgroup that left its loop on an empty ring
+    """Hundreds of back-to-back tiled calls (forward, reverse, backward) at the headline shape
+    (8, 1024, 65536): outputs filled with NaN before each call come back finite every time, no
+    wait gives up, and the last call equals the first bit for bit. A workgroup that left its loop on an empty ring
     while claims were still in flight dropped the tiles those claims held (their outputs were
     never written and the later tiles of their rows gave up waiting), a few calls in a
     hundred; the loop now ends only on the claim stream's end."""
     g, x, go = bench.make_inputs(8, 1024, 65536, dtype, "mamba", seed=21)
     y = fpscan_amd.scan_forward(g, x)
-    outs = [torch.empty_like(x)] if op == "fwd" else [torch.empty_like(x), torch.empty_like(x)]
+    outs = [torch.empty_like(x)] if op != "bwd" else [torch.empty_like(x), torch.empty_like(x)]
     nan_seen = torch.zeros((), dtype=torch.bool, device=DEVICE)
     first = None
     torch.cuda.synchronize()
@@ -269,8 +271,8 @@ def test_repeated_headline_calls_drop_no_tile(dtype, op, calls):
     for i in range(calls):
         for o in outs:
             o.fill_(float("nan"))
-        if op == "fwd":
-            fpscan_amd.scan_forward(g, x, False, outs[0])
+        if op != "bwd":
+            fpscan_amd.scan_forward(g, x, op == "rev", outs[0])
         else:
             fpscan_amd.scan_backward(g, y, go, outs[0], outs[1])
         for o in outs:
