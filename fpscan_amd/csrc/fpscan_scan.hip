@@ -914,8 +914,11 @@ constexpr int64_t kLongRowBytes = 64ll << 10;
 // Rows of one tile (16 sub-chunks) stream as 8-wave rows, which keep up with the tiles to
 // about 1 GiB per tensor: at 512 MiB streaming measured 3-8 % faster (bf16 32768 rows of L8192
 // forward / backward 255 / 420 us against 261-278 / 438; fp32 32768 rows of L4096 256 / 428
-// against 267 / 459), at 1 GiB the tiles 2.5 % faster forward (509 against 522 us) and even
-// backward.
+// against 267 / 459), at 1 GiB the tiles 2.5 % faster forward (509 against 522 us). The
+// 2-byte backward on such rows streams at every size: with the backward's claim groups served
+// by every XCD (same buffers, alternated, median of 5) bf16 L8192 streamed 854.5 against 872.1
+// us at 1 GiB and 1745.9 against 1809.5 at 2 GiB, while the fp32 backward on L4096 rows tiled
+// 842.8 against 847.2 and 1716.0 against 1772.8.
 constexpr int64_t kTiledMinBytesOneTileRows = 1ll << 30;
 
 struct TilePlan {
@@ -934,6 +937,7 @@ TilePlan plan_tiles(int64_t rows, int64_t seqlen, int size, int tiling, bool bwd
   if (tiling == 1 || nsub < kTileWaves) return t;
   t.tpr = (int)(nsub / kTileWaves);
   if (t.tpr > 64) return t;
+  if (tiling == 0 && t.tpr == 1 && bwd && size == 2) return t;  // streams at every size
   const int64_t min_bytes =
       t.tpr == 1 ? kTiledMinBytesOneTileRows
                  : (bwd && seqlen * size >= kLongRowBytes ? kTiledMinBytesBwdLongRows

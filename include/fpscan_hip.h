@@ -245,7 +245,7 @@ int fpscan_set_launch_override(int waves_per_row, int ring_depth);
 /* Path selection for tests and tuning (a test hook); process-wide, not synchronised with
  * calls in flight. 0: automatic (rows: tiled for problems
  * of at least 512 MiB per tensor, backward from 256 MiB with rows of 64 KiB or more, rows
- * of exactly 16 sub-chunks from 1 GiB;
+ * of exactly 16 sub-chunks from 1 GiB except the 2-byte backward, which streams them;
  * channel-last: tiled look-back when one pass per strip lacks strips or from 512 MiB per
  * tensor), 1: no tiled look-back (rows streamed; channel-last one
  * pass or segments), 2: tiled whenever possible (rows with 16..1024 sub-chunks; any
