@@ -602,9 +602,9 @@ scan_tiles(const Args a, uint64_t* __restrict__ status, const int tpr_log2, cons
   // the groups advance at the XCDs' mean speed and end together instead of waiting for the
   // slowest XCD's group. A/B on MI355X (same buffers, alternated, median of 7, tiled calls at
   // D1024 L65536): backward B8 bf16 888.8 -> 881.1 us, fp32 1768.5 -> 1715.1, B4 431.9 ->
-  // 425.8 / 918.1 -> 858.1, B2 bf16 234.1 -> 216.9, B1 fp32 238.3 -> 223.6; the forward
-  // loses with it (B8 fp32 1012.4 -> 1057.6: its shorter steps wait on words published
-  // across the device).
+  // 425.8 / 918.1 -> 858.1, B2 bf16 234.1 -> 216.9, B1 fp32 238.3 -> 223.6. The forward
+  // loses with it (B8 fp32 1012.4 -> 1057.6); timestamps per step phase put that loss in the
+  // waits for operand data, not in the look-back, which polls as rarely either way.
   const int first_group = kMode == kBwd ? (int)((blockIdx.x / kClaimGroups) % kClaimGroups)
                                         : (int)(blockIdx.x % kClaimGroups);
   Claims<RowGroups> claims{(uint32_t)((ntiles + kCounterStride) * sizeof(uint64_t)),
