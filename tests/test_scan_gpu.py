@@ -465,7 +465,7 @@ def _bench_inputs(batch, dim, seqlen, dtype, dist, seed):
     return bench.make_inputs(batch, dim, seqlen, dtype, dist, seed=seed, device=DEVICE)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
 def test_config4_headline_b8_d1024_l65536(dtype):
     g, x, go = _bench_inputs(8, 1024, 65536, dtype, "mamba", seed=4)
     _properties(g, x, go, rows_checked=48)
