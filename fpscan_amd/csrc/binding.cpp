@@ -67,6 +67,35 @@ at::Tensor workspace(size_t bytes, const at::Tensor& like) {
   return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
 }
 
+// Whether two contiguous tensors share any byte: [data_ptr, data_ptr + nbytes) intersect.
+bool overlap(const at::Tensor& a, const at::Tensor& b) {
+  const char* pa = static_cast<const char*>(a.data_ptr());
+  const char* pb = static_cast<const char*>(b.data_ptr());
+  return a.nbytes() > 0 && b.nbytes() > 0 && pa < pb + b.nbytes() && pb < pa + a.nbytes();
+}
+
+// An output that may be one of its inputs exactly (each element is read by the lane that
+// writes it) but must not overlap one partly, where a lane would overwrite elements that
+// another lane has still to read.
+void check_in_place(const at::Tensor& out, std::initializer_list<const at::Tensor*> inputs,
+                    const char* op) {
+  for (const at::Tensor* i : inputs)
+    TORCH_CHECK(out.data_ptr() == i->data_ptr() || !overlap(out, *i), op, ": out must be one "
+                "of its inputs or not overlap them (it may not alias an input partly)");
+}
+
+// Outputs that share no byte with the inputs or with each other: the kernels read
+// neighbouring elements (gates[t+1], out[t-1]) while other lanes write.
+void check_no_alias(std::initializer_list<const at::Tensor*> outputs,
+                    std::initializer_list<const at::Tensor*> inputs, const char* op) {
+  for (const at::Tensor* o : outputs)
+    for (const at::Tensor* i : inputs)
+      TORCH_CHECK(!overlap(*o, *i), op, " outputs must not alias its inputs");
+  for (auto a = outputs.begin(); a != outputs.end(); ++a)
+    for (auto b = a + 1; b != outputs.end(); ++b)
+      TORCH_CHECK(!overlap(**a, **b), op, " outputs must be distinct and must not overlap");
+}
+
 void check_status(int status) {
   TORCH_CHECK(status == FPSCAN_OK, "fpscan: ", fpscan_strerror(status), " (status ", status,
               ")");
@@ -96,6 +125,7 @@ at::Tensor fullscan_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at
   check_input(out, "out");
   check_like(out, Bx, "out", "Bx");
   check_seqlen(Bx.size(2));
+  check_in_place(out, {&Ax, &Bx}, "fullscan_forward");
   if (Bx.numel() == 0) return out;
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
@@ -129,16 +159,7 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward(const at::Tensor& gates,
   check_like(grad_tokens, gates, "grad_tokens", "gates");
   check_seqlen(gates.size(2));
   if (gates.numel() == 0) return {grad_gates, grad_tokens};
-  // the kernel reads neighbouring rows' boundary values (gates[t+1], out[t-1]) while other
-  // waves write, so no output may share memory with an input or with the other output
-  for (const at::Tensor* o : {&grad_gates, &grad_tokens}) {
-    for (const at::Tensor* i : {&gates, &out, &grad_out}) {
-      TORCH_CHECK(o->data_ptr() != i->data_ptr(), "fullscan_backward outputs must not alias "
-                  "its inputs");
-    }
-  }
-  TORCH_CHECK(grad_gates.data_ptr() != grad_tokens.data_ptr(),
-              "grad_gates and grad_tokens must be distinct");
+  check_no_alias({&grad_gates, &grad_tokens}, {&gates, &out, &grad_out}, "fullscan_backward");
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(gates.device());
   void* stream = launch_stream(gates);
@@ -206,6 +227,7 @@ at::Tensor fullscan_forward_cl(const at::Tensor& Ax, const at::Tensor& Bx, const
   check_like(Ax, Bx, "Ax", "Bx");
   check_input_cl(out, "out");
   check_like(out, Bx, "out", "Bx");
+  check_in_place(out, {&Ax, &Bx}, "fullscan_forward_cl");
   if (Bx.numel() == 0) return out;
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
@@ -236,15 +258,7 @@ std::tuple<at::Tensor, at::Tensor> fullscan_backward_cl(const at::Tensor& gates,
   check_like(grad_gates, gates, "grad_gates", "gates");
   check_like(grad_tokens, gates, "grad_tokens", "gates");
   if (gates.numel() == 0) return {grad_gates, grad_tokens};
-  // neighbouring time steps are read (gates[t+1], out[t-1]) while other waves write
-  for (const at::Tensor* o : {&grad_gates, &grad_tokens}) {
-    for (const at::Tensor* i : {&gates, &out, &grad_out}) {
-      TORCH_CHECK(o->data_ptr() != i->data_ptr(), "fullscan_backward_cl outputs must not "
-                  "alias its inputs");
-    }
-  }
-  TORCH_CHECK(grad_gates.data_ptr() != grad_tokens.data_ptr(),
-              "grad_gates and grad_tokens must be distinct");
+  check_no_alias({&grad_gates, &grad_tokens}, {&gates, &out, &grad_out}, "fullscan_backward_cl");
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(gates.device());
   void* stream = launch_stream(gates);
@@ -289,6 +303,9 @@ void dimwise_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tenso
               Bh.sizes());
   TORCH_CHECK(Wq.numel() == D && Wk.numel() == D, "Wq and Wk must have ", D,
               " elements (one per dim), got ", Wq.numel(), " and ", Wk.numel());
+  // Bx is the output: Ax may be Bx itself, the per-row parameters must lie apart from it
+  check_in_place(Bx, {&Ax}, "dimwise_forward");
+  check_no_alias({&Bx}, {&Bh, &Wq, &Wk}, "dimwise_forward");
   if (Bx.numel() == 0) return;
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
@@ -319,6 +336,7 @@ at::Tensor fullscan_forward_softplus(const at::Tensor& z, const at::Tensor& rate
   check_like(out, tokens, "out", "tokens");
   check_rate(rate, tokens, "rate");
   check_seqlen(tokens.size(2));
+  check_in_place(out, {&z, &tokens}, "fullscan_forward_softplus");
   if (tokens.numel() == 0) return out;
   c10::hip::HIPGuardMasqueradingAsCUDA guard(tokens.device());
   void* stream = launch_stream(tokens);
@@ -352,14 +370,8 @@ void fullscan_backward_softplus(const at::Tensor& z, const at::Tensor& rate,
               "grad_rate_rows must be a contiguous float32 tensor with batch*dim (", rows,
               ") elements");
   if (z.numel() == 0) return;
-  for (const at::Tensor* o : {&grad_z, &grad_tokens}) {
-    for (const at::Tensor* i : {&z, &out, &grad_out}) {
-      TORCH_CHECK(o->data_ptr() != i->data_ptr(), "fullscan_backward_softplus outputs must not "
-                  "alias its inputs");
-    }
-  }
-  TORCH_CHECK(grad_z.data_ptr() != grad_tokens.data_ptr(),
-              "grad_z and grad_tokens must be distinct");
+  check_no_alias({&grad_z, &grad_tokens, &grad_rate_rows}, {&z, &rate, &out, &grad_out},
+                 "fullscan_backward_softplus");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(z.device());
   void* stream = launch_stream(z);
   const int64_t D = z.size(1), L = z.size(2);

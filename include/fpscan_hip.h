@@ -85,7 +85,8 @@ extern "C" {
  * Replaces warpscan_fwd / warpscan_forward (csrc/full_scan/full_scan.h:26-36,
  * csrc/full_scan/full_scan.cu:238-258); `gates`/`tokens` are the reference's Ax/Bx and
  * `out` is written in full (the reference's caller allocates it, fpscan/ops.py:55-56).
- * `out` may alias `tokens` or `gates` exactly (in-place scan). */
+ * `out` may alias `tokens` or `gates` exactly (in-place scan), never partly: the library does
+ * not check pointer ranges (the torch binding refuses partial overlaps). */
 int fpscan_scan_fwd(const void* gates, const void* tokens, void* out,
                     int64_t batch, int64_t dim, int64_t seqlen,
                     int64_t stride_b, int64_t stride_d,

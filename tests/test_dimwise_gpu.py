@@ -127,6 +127,14 @@ def test_empty_and_validation():
         fpscan_amd.dimwise_forward(x, x.clone().transpose(0, 1), bh, w, w)
     with pytest.raises(RuntimeError, match="CUDA"):
         fpscan_amd.dimwise_forward(x.cpu(), x.clone(), bh, w, w)
+    # Bx is written in place: Ax may be Bx itself but not part of it, and the per-row
+    # parameters must not lie inside it
+    buf = torch.rand(2 * 3 * 64 + 64, device=DEVICE)
+    with pytest.raises(RuntimeError, match="alias"):
+        fpscan_amd.dimwise_forward(buf[64:].view(2, 3, 64), buf[:-64].view(2, 3, 64), bh, w, w)
+    bx = x.clone()
+    with pytest.raises(RuntimeError, match="alias"):
+        fpscan_amd.dimwise_forward(x, bx, bh, bx.view(-1)[:3], w)
     assert fpscan_amd.dimwise_groups(65536) == 512 and fpscan_amd.dimwise_groups(32) == 0
 
 

@@ -89,6 +89,44 @@ def test_in_place_at_the_automatic_tiling_size():
         del gi, xi, target
 
 
+def test_partial_overlaps_are_refused_before_any_launch():
+    """An output may be one of its inputs exactly (forward scans) but never part of one, and
+    backward outputs share no byte with inputs or each other: a lane would overwrite elements
+    another lane still reads (the backward reads gates[t+1] and out[t-1] across lanes)."""
+    shape, n = (2, 4, 64), 2 * 4 * 64
+    buf = torch.randn(n + 64, device=DEVICE)
+    a, shifted = buf[:n].view(shape), buf[64:n + 64].view(shape)  # overlap by 7 of 8 rows
+    x = torch.randn(shape, device=DEVICE)
+    keep = buf.clone()
+    with pytest.raises(RuntimeError, match="alias"):
+        fpscan_amd.scan_forward(a, x, out=shifted)
+    with pytest.raises(RuntimeError, match="alias"):
+        fpscan_amd.scan_forward(x, a, out=shifted)
+    y = fpscan_amd.scan_forward(x, x.clone())
+    go = torch.randn_like(y)
+    with pytest.raises(RuntimeError, match="alias"):
+        fpscan_amd.scan_backward(a, y, go, grad_gates=shifted, grad_tokens=torch.empty_like(y))
+    with pytest.raises(RuntimeError, match="overlap"):
+        fpscan_amd.scan_backward(x, y, go, grad_gates=a, grad_tokens=shifted)
+    # channel-last (batch, seqlen, dim) and the fused gates
+    cl = (2, 8, 32)
+    a_cl, s_cl = buf[:n].view(cl), buf[64:n + 64].view(cl)
+    with pytest.raises(RuntimeError, match="alias"):
+        fpscan_amd.scan_forward_channel_last(a_cl, torch.randn(cl, device=DEVICE), out=s_cl)
+    with pytest.raises(RuntimeError, match="overlap"):
+        fpscan_amd.scan_backward_channel_last(x.view(cl), y.view(cl), go.view(cl),
+                                              grad_gates=a_cl, grad_tokens=s_cl)
+    rate = torch.ones(4, device=DEVICE)
+    with pytest.raises(RuntimeError, match="alias"):
+        fpscan_amd.scan_forward_softplus(a, rate, x, out=shifted)
+    torch.cuda.synchronize()
+    assert torch.equal(buf, keep), "a refused call wrote into its outputs"
+    # exact aliasing stays allowed
+    want = fpscan_amd.scan_forward(a.clone(), x)
+    fpscan_amd.scan_forward(a, x, out=a)
+    assert bits_equal(a, want)
+
+
 # ------------------------------------------------------------------ look-back waits that give up
 def _tile_span(seg, tile_len, L, reverse):
     """Element range [lo, hi) of tile `seg` of a row, in memory order."""
