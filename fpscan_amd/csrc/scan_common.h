@@ -407,14 +407,14 @@ struct RowGroups {
 // each (whole rows, or whole chains of the channel-last scan, per group: `Groups`). A
 // workgroup starts in the group its kernel picks (most: blockIdx % kClaimGroups, its XCD
 // under round-robin dispatch) and, when that one is used up, moves to the group with the most
-// tiles left. A
-// row never spans two groups and tiles of a group are claimed in order, so a tile's
-// predecessors are always claimed before it. Claims are issued two steps before their tile
-// is needed (an atomic at the memory side takes a few microseconds under full streaming
-// load), so each claim is kept with the group it was made in. In the main loop every lane of every wave issues the claim as a
-// buffer atomic that is out of range except in the leader's lane: a claim inside a branch, or
-// any use of its result before it is resolved, makes the compiler wait for it together with
-// every load issued before it. Counters are the low 32 bits of their words.
+// tiles left. A row never spans two groups and tiles of a group are claimed in order, so a
+// tile's predecessors are always claimed before it. Claims are issued two steps before their
+// tile is needed (an atomic at the memory side takes a few microseconds under full streaming
+// load), so each claim is kept with the group it was made in. In the main loop every lane of
+// every wave issues the claim as a buffer atomic that is out of range except in the leader's
+// lane: a claim inside a branch, or any use of its result before it is resolved, makes the
+// compiler wait for it together with every load issued before it. Counters are the low 32
+// bits of their words.
 struct Claim {
   uint32_t raw;
   int grp;

@@ -34,9 +34,9 @@
  * of counters, about 0.05 % of one tensor). Pass a buffer of at least that size, 8-byte
  * aligned, owned by the caller and not used by any other call in flight. Its contents are
  * overwritten. With no workspace (or a smaller one) the call takes the row-streaming path
- * instead: same results up to fp32 rounding order, somewhat lower bandwidth. The tiled path is an ordinary launch that
- * needs no co-residency (workgroups claim tiles in order); if the occupancy query fails, the
- * call streams rows.
+ * instead: same results up to fp32 rounding order, somewhat lower bandwidth. The tiled path
+ * is an ordinary launch that needs no co-residency (workgroups claim tiles in order); if the
+ * occupancy query fails, the call streams rows.
  *
  * Reference interface replaced (saeeddhqan/fpscan):
  *   csrc/main.cpp:7-11              PYBIND11_MODULE: "fullscan_forward" -> warpscan_fwd
