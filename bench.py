@@ -926,7 +926,61 @@ def bench_ceiling(args):
         del gates, tokens, grad_out, out, y, gg, gx
         print(json.dumps(entry), flush=True)
         res["cases"].append(entry)
+    res["channel_last"] = _ceiling_channel_last(lib, args.iters)
     return res
+
+
+def _ceiling_channel_last(lib, iters):
+    """The channel-last tiled scan's pattern (fpscan_probe_copy_cl: chains of 64 columns, 16
+    KiB tiles of one chain claimed per chain group) beside the channel-last scans, bf16
+    (batch, 65536, 1024): batch 8 (128 chains, 1 GiB per tensor) and batch 1 (16 chains)."""
+    import ctypes
+
+    import fpscan_amd
+
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_probe_copy_cl.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, i64, i64, i64,
+                                         ctypes.c_int, vp, ctypes.c_size_t, vp]
+    lib.fpscan_probe_copy_cl.restype = ctypes.c_int
+    out = []
+    for B in (8, 1):
+        L, D, dtype = 65536, 1024, torch.bfloat16
+        s = 2
+        tensor_bytes = B * L * D * s
+        entry = {"case": f"channel-last ({B}, {L}, {D}) bf16", "chains": B * D // 64,
+                 "tensor_bytes": tensor_bytes, "probes": {}}
+        src = torch.ones(3 * tensor_bytes, dtype=torch.uint8, device="cuda")
+        dst = torch.empty(2 * tensor_bytes, dtype=torch.uint8, device="cuda")
+        scratch_bytes = lib.fpscan_probe_scratch_bytes()
+        scratch = torch.zeros(scratch_bytes, dtype=torch.uint8, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        for nr, nw in ((2, 1), (3, 2)):
+            def call():
+                st = lib.fpscan_probe_copy_cl(nr, nw, src.data_ptr(), dst.data_ptr(), B, L, D * s,
+                                              128, scratch.data_ptr(), scratch_bytes, stream)
+                if st != 0:
+                    raise RuntimeError(f"fpscan_probe_copy_cl status {st}")
+            e = _timed_entry(call, (nr + nw) * tensor_bytes, iters)
+            entry["probes"][f"cl_tiles_{nr}r{nw}w"] = {k: e[k] for k in ("p50_ms", "gbps",
+                                                                          "hbm_frac")}
+        del src, dst, scratch
+        gen = torch.Generator(device="cuda").manual_seed(3)
+        g = (0.99 + 0.01 * torch.rand(B, L, D, generator=gen, device="cuda")).to(dtype)
+        x = (torch.randn(B, L, D, generator=gen, device="cuda") / L).to(dtype)
+        go = torch.randn(B, L, D, generator=gen, device="cuda").to(dtype)
+        y = fpscan_amd.scan_forward_channel_last(g, x)
+        o = torch.empty_like(x)
+        gg, gx = torch.empty_like(g), torch.empty_like(g)
+        fwd = _timed_entry(lambda: fpscan_amd.scan_forward_channel_last(g, x, False, o),
+                           3 * tensor_bytes, iters)
+        bwd = _timed_entry(lambda: fpscan_amd.scan_backward_channel_last(g, y, go, gg, gx),
+                           5 * tensor_bytes, iters)
+        entry["scan"] = {"fwd": {k: fwd[k] for k in ("p50_ms", "gbps", "hbm_frac")},
+                         "bwd": {k: bwd[k] for k in ("p50_ms", "gbps", "hbm_frac")}}
+        del g, x, go, y, o, gg, gx
+        print(json.dumps(entry), flush=True)
+        out.append(entry)
+    return out
 
 
 def main():

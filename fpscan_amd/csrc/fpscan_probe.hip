@@ -16,6 +16,11 @@
 //   BLOCKS_LOOKBACK  256-thread blocks of 16 KiB tiles in memory order, each waiting before its
 //           stores until every earlier tile of its row has loaded its data: the wait a
 //           single-pass scan in memory order needs.
+//   channel-last tiles (fpscan_probe_copy_cl): (batch, seqlen, dim) tensors cut into chains of
+//           64 columns over all time rows and tiles of 16 KiB of one chain (128 time rows of
+//           128-byte strips, or 64 of 256-byte strips), claimed like TILES but per chain
+//           group, all of a group's chains' first tiles, then their second ones, and so on;
+//           lanes hold consecutive 16-byte pieces of a time row (the channel-last tiled scan).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -40,25 +45,81 @@ __device__ __forceinline__ void combine_store(const u32x4 (&v)[NR], const Rsrc (
   }
 }
 
-template <int NR, int NW>
+// Tile geometries of probe_tiles: the claim groups, where a tile lies in a tensor and this
+// lane's byte offset in it.
+// Row tiles: 16 KiB contiguous, groups of contiguous eighths.
+struct RowTileGeo {
+  int64_t ntiles;
+  __device__ RowGroups groups() const { return RowGroups{ntiles, 0}; }
+  __device__ uint32_t lane_off() const { return threadIdx.x * 16u; }
+  __device__ Rsrc rsrc(const char* base, int64_t t) const {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + t * kTileBytes, (short)0,
+                                             kTileBytes, kRsrcWord3);
+  }
+};
+
+// Claim groups over chains (the channel-last scan's): group g holds chains
+// [g chains / 8, (g + 1) chains / 8), tiles numbered segment-major inside a group.
+struct ChainTileGroups {
+  int64_t chains;
+  int64_t nseg;
+  __device__ int64_t chain_lo(int g) const {
+    return (int64_t)(((uint64_t)g * (uint64_t)chains) / kClaimGroups);
+  }
+  __device__ int64_t first(int g) const { return chain_lo(g) * nseg; }
+};
+
+// Channel-last tiles: chain = (batch, strip of strip_bytes), tile = tile_rows time rows of
+// one chain; lane l of wave w holds piece l % pieces of time row w * (64 / pieces) + l / pieces.
+struct ClTileGeo {
+  int64_t seqlen;
+  int64_t row_bytes;  // one time row of one batch
+  int64_t strips;     // chains per batch
+  int strip_bytes;    // 128 or 256
+  int tile_rows;      // 16 KiB / strip_bytes
+  ChainTileGroups cg;
+  __device__ ChainTileGroups groups() const { return cg; }
+  __device__ uint32_t lane_off() const {
+    const int pieces = strip_bytes >> 4;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    return (uint32_t)((w * (64 / pieces) + lane / pieces) * row_bytes + (lane % pieces) * 16);
+  }
+  __device__ Rsrc rsrc(const char* base, int64_t t) const {
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < kClaimGroups; ++i) g += t >= cg.first(i) ? 1 : 0;
+    const int64_t c_lo = cg.chain_lo(g);
+    const uint32_t nch = (uint32_t)(cg.chain_lo(g + 1) - c_lo);
+    const uint32_t k = (uint32_t)(t - c_lo * cg.nseg);
+    // uniform integer divisions run on the vector unit: bring the results back to scalars
+    const uint32_t seg = __builtin_amdgcn_readfirstlane(k / nch);
+    const int64_t chain = c_lo + (int64_t)(k - seg * nch);
+    const uint32_t b = __builtin_amdgcn_readfirstlane((uint32_t)chain / (uint32_t)strips);
+    const int64_t strip = chain - (int64_t)b * strips;
+    const int64_t start = ((int64_t)b * seqlen + (int64_t)seg * tile_rows) * row_bytes +
+                          strip * strip_bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(base) + start, (short)0,
+        (int)((int64_t)(tile_rows - 1) * row_bytes + strip_bytes), kRsrcWord3);
+  }
+};
+
+template <int NR, int NW, class Geo>
 __global__ void __launch_bounds__(1024)
 probe_tiles(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes,
-            uint64_t* __restrict__ status, int64_t ntiles) {
+            uint64_t* __restrict__ status, int64_t ntiles, const Geo geo) {
   const bool leader = threadIdx.x == 0;
-  const uint32_t lane_off = threadIdx.x * 16u;
+  const uint32_t lane_off = geo.lane_off();
   const Rsrc st = __builtin_amdgcn_make_buffer_rsrc(
       status, (short)0, (int)(kStatusExtraWords * sizeof(uint64_t)), kRsrcWord3);
   // the status buffer holds no tile words here: the counters start at word kCounterStride
-  Claims<RowGroups> claims{(uint32_t)(kCounterStride * sizeof(uint64_t)),
-                           reinterpret_cast<const uint32_t*>(status + kCounterStride),
-                           RowGroups{ntiles, 0}, (int)(blockIdx.x % kClaimGroups)};
+  Claims<decltype(geo.groups())> claims{(uint32_t)(kCounterStride * sizeof(uint64_t)),
+                                        reinterpret_cast<const uint32_t*>(status + kCounterStride),
+                                        geo.groups(), (int)(blockIdx.x % kClaimGroups)};
   const int64_t kBubble = ntiles, kDone = ntiles + 1;
   __shared__ int64_t next_tile;
 
-  auto tile_rsrc = [&](const char* base, int64_t t) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + t * kTileBytes, (short)0,
-                                             kTileBytes, kRsrcWord3);
-  };
+  auto tile_rsrc = [&](const char* base, int64_t t) { return geo.rsrc(base, t); };
   auto load = [&](int64_t t, u32x4 (&v)[NR]) {
     const int64_t tt = t < ntiles ? t : 0;
     const uint32_t off = t < ntiles ? lane_off : kNoOffset;
@@ -222,6 +283,28 @@ probe_rows(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_
   }
 }
 
+// The persistent grid of probe_tiles over `geo`: one workgroup per resident slot, after a
+// clear of the claim counters on the same stream.
+template <int NR, int NW, class Geo>
+int launch_tiles(const char* s, char* d, int64_t tensor_bytes, int64_t ntiles, const Geo& geo,
+                 void* scratch, hipStream_t stream) {
+  uint64_t* status = static_cast<uint64_t*>(scratch);
+  int64_t zero = 0;
+  hipLaunchKernelGGL(clear_status, dim3(1), dim3(256), 0, stream, status, zero);
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void*>(&probe_tiles<NR, NW, Geo>), 1024, 0) !=
+          hipSuccess ||
+      cus <= 0 || per_cu <= 0)
+    return FPSCAN_PROBE_ERR_DEVICE;
+  const int64_t grid = (int64_t)cus * per_cu < ntiles ? (int64_t)cus * per_cu : ntiles;
+  hipLaunchKernelGGL((probe_tiles<NR, NW, Geo>), dim3((unsigned)grid), dim3(1024), 0, stream, s,
+                     d, tensor_bytes, status, ntiles, geo);
+  return hipGetLastError() == hipSuccess ? FPSCAN_PROBE_OK : FPSCAN_PROBE_ERR_LAUNCH;
+}
+
 template <int NR, int NW>
 int launch_probe(int pattern, const void* src, void* dst, int64_t tensor_bytes, int64_t row_bytes,
                  void* scratch, hipStream_t stream) {
@@ -243,20 +326,8 @@ int launch_probe(int pattern, const void* src, void* dst, int64_t tensor_bytes, 
     hipLaunchKernelGGL((probe_rows<NR, NW>), dim3((unsigned)(tensor_bytes / row_bytes)),
                        dim3(1024), 0, stream, s, d, tensor_bytes, row_bytes);
   } else {
-    uint64_t* status = static_cast<uint64_t*>(scratch);
-    int64_t zero = 0;
-    hipLaunchKernelGGL(clear_status, dim3(1), dim3(256), 0, stream, status, zero);
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&probe_tiles<NR, NW>), 1024, 0) != hipSuccess ||
-        cus <= 0 || per_cu <= 0)
-      return FPSCAN_PROBE_ERR_DEVICE;
     const int64_t ntiles = tensor_bytes / kTileBytes;
-    const int64_t grid = (int64_t)cus * per_cu < ntiles ? (int64_t)cus * per_cu : ntiles;
-    hipLaunchKernelGGL((probe_tiles<NR, NW>), dim3((unsigned)grid), dim3(1024), 0, stream, s, d,
-                       tensor_bytes, status, ntiles);
+    return launch_tiles<NR, NW>(s, d, tensor_bytes, ntiles, RowTileGeo{ntiles}, scratch, stream);
   }
   return hipGetLastError() == hipSuccess ? FPSCAN_PROBE_OK : FPSCAN_PROBE_ERR_LAUNCH;
 }
@@ -302,6 +373,38 @@ int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void*
   hipStream_t s = static_cast<hipStream_t>(stream);
   return nread == 2 ? launch_probe<2, 1>(pattern, src, dst, tensor_bytes, row_bytes, scratch, s)
                     : launch_probe<3, 2>(pattern, src, dst, tensor_bytes, row_bytes, scratch, s);
+}
+
+int fpscan_probe_copy_cl(int nread, int nwrite, const void* src, void* dst, int64_t batch,
+                         int64_t seqlen, int64_t row_bytes, int strip_bytes, void* scratch,
+                         size_t scratch_bytes, void* stream) {
+  if (!((nread == 2 && nwrite == 1) || (nread == 3 && nwrite == 2))) return FPSCAN_PROBE_ERR_ARG;
+  if (src == nullptr || dst == nullptr || scratch == nullptr ||
+      scratch_bytes < fpscan_probe_scratch_bytes())
+    return FPSCAN_PROBE_ERR_ARG;
+  if ((reinterpret_cast<uintptr_t>(src) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(dst) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(scratch) & 7u) != 0)
+    return FPSCAN_PROBE_ERR_ARG;
+  if (strip_bytes != 128 && strip_bytes != 256) return FPSCAN_PROBE_ERR_ARG;
+  const int tile_rows = kTileBytes / strip_bytes;
+  if (batch <= 0 || seqlen <= 0 || seqlen % tile_rows != 0 || row_bytes <= 0 ||
+      row_bytes % strip_bytes != 0)
+    return FPSCAN_PROBE_ERR_ARG;
+  const int64_t tensor_bytes = batch * seqlen * row_bytes;
+  // at most 4 GiB per tensor and a tile's range below 2 GiB (32-bit buffer offsets)
+  if (tensor_bytes > (int64_t)1 << 32 || (int64_t)tile_rows * row_bytes > INT32_MAX)
+    return FPSCAN_PROBE_ERR_ARG;
+  const int64_t strips = row_bytes / strip_bytes;
+  const int64_t nseg = seqlen / tile_rows;
+  const int64_t ntiles = batch * strips * nseg;
+  const ClTileGeo geo{seqlen, row_bytes, strips, strip_bytes, tile_rows,
+                      ChainTileGroups{batch * strips, nseg}};
+  const char* s = static_cast<const char*>(src);
+  char* d = static_cast<char*>(dst);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return nread == 2 ? launch_tiles<2, 1>(s, d, tensor_bytes, ntiles, geo, scratch, st)
+                    : launch_tiles<3, 2>(s, d, tensor_bytes, ntiles, geo, scratch, st);
 }
 
 }  // extern "C"

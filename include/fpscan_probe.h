@@ -54,6 +54,18 @@ int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void*
                       int64_t tensor_bytes, int64_t row_bytes, void* scratch,
                       size_t scratch_bytes, void* stream);
 
+/* The channel-last tiled scan's pattern (fpscan_scan_fwd_cl / _bwd_cl on the tiled path):
+ * tensors of `batch` x `seqlen` time rows of row_bytes (a (batch, seqlen, dim) tensor with
+ * row_bytes = dim * itemsize), cut into chains of strip_bytes columns (128: 64 columns of a
+ * 2-byte type; 256: 64 fp32 columns) over all time rows and tiles of 16 KiB of one chain,
+ * claimed by a persistent grid from 8 counters, one per eighth of the chains, all of a
+ * group's chains' first tiles first; two tiles in flight per workgroup. Same outputs as
+ * fpscan_probe_copy. seqlen a multiple of 16 KiB / strip_bytes; row_bytes a multiple of
+ * strip_bytes; at most 4 GiB per tensor; scratch as for FPSCAN_PROBE_TILES. */
+int fpscan_probe_copy_cl(int nread, int nwrite, const void* src, void* dst, int64_t batch,
+                         int64_t seqlen, int64_t row_bytes, int strip_bytes, void* scratch,
+                         size_t scratch_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,7 +81,8 @@ def test_probe_rejects_bad_arguments_before_any_launch(lib):
     assert lib.fpscan_probe_scratch_bytes() == 8 * 16 * 9
     buf, kib16 = 1 << 20, 16 << 10
     bad = [
-        (3, 2, 1, buf, buf, kib16, 0, None, 0),        # unknown pattern
+        (7, 2, 1, buf, buf, kib16, 0, None, 0),        # unknown pattern
+        (3, 2, 1, buf, buf, kib16, kib16, None, 0),    # look-back blocks without scratch
         (1, 2, 2, buf, buf, kib16, 0, None, 0),        # (2, 2) is not a scan's traffic
         (1, 2, 1, None, buf, kib16, 0, None, 0),       # null source
         (1, 2, 1, buf + 8, buf, kib16, 0, None, 0),    # misaligned
@@ -93,6 +94,23 @@ def test_probe_rejects_bad_arguments_before_any_launch(lib):
     ]
     for args in bad:
         assert lib.fpscan_probe_copy(*args, None) == 1, args
+    lib.fpscan_probe_copy_cl.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, i64, i64, i64,
+                                         ctypes.c_int, vp, ctypes.c_size_t, vp]
+    lib.fpscan_probe_copy_cl.restype = ctypes.c_int
+    scratch = lib.fpscan_probe_scratch_bytes()
+    bad_cl = [
+        (2, 2, buf, buf, 1, 128, 2048, 128, buf, scratch),     # (2, 2) traffic
+        (2, 1, buf, buf, 1, 129, 2048, 128, buf, scratch),     # not whole 128-row tiles
+        (2, 1, buf, buf, 1, 64, 2048, 256, buf + 4, scratch),  # misaligned scratch
+        (2, 1, buf, buf, 1, 128, 2048, 64, buf, scratch),      # strips of 64 bytes
+        (2, 1, buf, buf, 1, 128, 2000, 128, buf, scratch),     # rows not whole strips
+        (2, 1, buf, buf, 0, 128, 2048, 128, buf, scratch),     # empty batch
+        (3, 2, buf, buf, 1, 128, 2048, 128, None, scratch),    # no scratch
+        (3, 2, buf, buf, 1, 128, 2048, 128, buf, 64),          # scratch too small
+        (2, 1, buf, buf, 2, 1 << 20, 4096, 128, buf, scratch),  # above 4 GiB
+    ]
+    for args in bad_cl:
+        assert lib.fpscan_probe_copy_cl(*args, None) == 1, args
 
 
 def test_abi_version_matches_header(lib):
