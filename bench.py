@@ -835,11 +835,36 @@ def bench_dimwise(args):
     entry = {"workload": "dw: dimwise_forward B8 D1024 L65536", "dtype": SHORT[dtype],
              "p50_ms": round(p50, 5), "gbps": round(3 * N * s / (p50 / 1e3) / 1e9, 1),
              "hbm_frac": round(3 * N * s / (p50 / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    # the copy of its access pattern (eight-wave rows, two 8 KiB rounds in flight, 2 reads +
+    # 1 write of the same tensor size), timed beside it
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(fpscan_amd.__file__), "libfpscan_hip.so"))
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.fpscan_probe_copy.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, i64, i64,
+                                      vp, ctypes.c_size_t, vp]
+    lib.fpscan_probe_copy.restype = ctypes.c_int
+    del ax, bx0, bh, wq, wk, bx
+    tensor_bytes = N * s
+    src = torch.ones(2 * tensor_bytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(tensor_bytes, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def probe():
+        st = lib.fpscan_probe_copy(PROBE_ROWS8, 2, 1, src.data_ptr(), dst.data_ptr(),
+                                   tensor_bytes, L * s, None, 0, stream)
+        if st != 0:
+            raise RuntimeError(f"fpscan_probe_copy status {st}")
+    e = _timed_entry(probe, 3 * tensor_bytes, args.iters)
+    entry["pattern_copy_rows8"] = {k: e[k] for k in ("p50_ms", "gbps", "hbm_frac")}
+    entry["of_pattern"] = round(entry["gbps"] / e["gbps"], 3)
+    del src, dst
     print(json.dumps(entry), flush=True)
     return entry
 
 
 PROBE_PATTERNS = {"tiles": 0, "blocks": 1, "rows": 2, "blocks_lookback": 3}  # fpscan_probe.h
+PROBE_ROWS8 = 4  # eight-wave rows, 8 KiB rounds, two in flight: dimwise_forward's pattern
 
 
 def bench_ceiling(args):

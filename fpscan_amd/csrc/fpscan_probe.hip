@@ -13,6 +13,8 @@
 //           (the pattern of the row scan on rows of one sub-chunk, one wave per row).
 //   ROWS    one 1024-thread workgroup per row of `row_bytes`, walked in 16 KiB rounds with four
 //           rounds in flight (the pattern of the row-streaming scan with 16 waves per row).
+//   ROWS8   one 512-thread workgroup per row, 8 KiB rounds, two in flight (the pattern of
+//           dimwise_forward and of the row scans with eight waves per row).
 //   BLOCKS_LOOKBACK  256-thread blocks of 16 KiB tiles in memory order, each waiting before its
 //           stores until every earlier tile of its row has loaded its data: the wait a
 //           single-pass scan in memory order needs.
@@ -252,20 +254,20 @@ probe_blocks_lookback(const char* __restrict__ src, char* __restrict__ dst, int6
   }
 }
 
-template <int NR, int NW>
-__global__ void __launch_bounds__(1024)
+template <int NR, int NW, int W, int U>
+__global__ void __launch_bounds__(64 * W)
 probe_rows(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes,
            int64_t row_bytes) {
-  constexpr int U = 4;
+  constexpr int kRoundBytes = W * 1024;  // one 16-byte vector per lane
   const int64_t base = (int64_t)blockIdx.x * row_bytes;
-  const int nrounds = (int)(row_bytes / kTileBytes);
+  const int nrounds = (int)(row_bytes / kRoundBytes);
   const uint32_t lane_off = threadIdx.x * 16u;
   Rsrc in[NR], out[NW];
 #pragma unroll
   for (int i = 0; i < NR; ++i) in[i] = row_rsrc(src + i * tensor_bytes, base, 1, (int)row_bytes);
 #pragma unroll
   for (int o = 0; o < NW; ++o) out[o] = row_rsrc(dst + o * tensor_bytes, base, 1, (int)row_bytes);
-  auto off_of = [&](int r) { return r < nrounds ? (uint32_t)r * kTileBytes + lane_off : kNoOffset; };
+  auto off_of = [&](int r) { return r < nrounds ? (uint32_t)r * kRoundBytes + lane_off : kNoOffset; };
   u32x4 ring[U][NR];
 #pragma unroll
   for (int u = 0; u < U; ++u)
@@ -323,8 +325,11 @@ int launch_probe(int pattern, const void* src, void* dst, int64_t tensor_bytes, 
     hipLaunchKernelGGL((probe_blocks_lookback<NR, NW>), dim3((unsigned)tiles), dim3(256), 0,
                        stream, s, d, tensor_bytes, row_tiles, static_cast<uint32_t*>(scratch), e);
   } else if (pattern == FPSCAN_PROBE_ROWS) {
-    hipLaunchKernelGGL((probe_rows<NR, NW>), dim3((unsigned)(tensor_bytes / row_bytes)),
+    hipLaunchKernelGGL((probe_rows<NR, NW, 16, 4>), dim3((unsigned)(tensor_bytes / row_bytes)),
                        dim3(1024), 0, stream, s, d, tensor_bytes, row_bytes);
+  } else if (pattern == FPSCAN_PROBE_ROWS8) {
+    hipLaunchKernelGGL((probe_rows<NR, NW, 8, 2>), dim3((unsigned)(tensor_bytes / row_bytes)),
+                       dim3(512), 0, stream, s, d, tensor_bytes, row_bytes);
   } else {
     const int64_t ntiles = tensor_bytes / kTileBytes;
     return launch_tiles<NR, NW>(s, d, tensor_bytes, ntiles, RowTileGeo{ntiles}, scratch, stream);
@@ -346,7 +351,8 @@ int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void*
                       int64_t tensor_bytes, int64_t row_bytes, void* scratch,
                       size_t scratch_bytes, void* stream) {
   if (pattern != FPSCAN_PROBE_TILES && pattern != FPSCAN_PROBE_BLOCKS &&
-      pattern != FPSCAN_PROBE_ROWS && pattern != FPSCAN_PROBE_BLOCKS_LOOKBACK)
+      pattern != FPSCAN_PROBE_ROWS && pattern != FPSCAN_PROBE_BLOCKS_LOOKBACK &&
+      pattern != FPSCAN_PROBE_ROWS8)
     return FPSCAN_PROBE_ERR_ARG;
   if (!((nread == 2 && nwrite == 1) || (nread == 3 && nwrite == 2))) return FPSCAN_PROBE_ERR_ARG;
   if (src == nullptr || dst == nullptr) return FPSCAN_PROBE_ERR_ARG;
@@ -355,7 +361,7 @@ int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void*
   // whole tiles; at most 4 GiB per tensor keeps every grid below 2^32 work-items
   if (tensor_bytes <= 0 || tensor_bytes % kTileBytes != 0 || tensor_bytes > (int64_t)1 << 32)
     return FPSCAN_PROBE_ERR_ARG;
-  if (pattern == FPSCAN_PROBE_ROWS &&
+  if ((pattern == FPSCAN_PROBE_ROWS || pattern == FPSCAN_PROBE_ROWS8) &&
       (row_bytes <= 0 || row_bytes % kTileBytes != 0 || tensor_bytes % row_bytes != 0 ||
        row_bytes > INT32_MAX))
     return FPSCAN_PROBE_ERR_ARG;

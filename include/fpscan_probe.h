@@ -25,6 +25,9 @@ extern "C" {
                                  order; after its loads a block publishes a word and waits
                                  (bounded) until every earlier tile of its row of row_bytes
                                  has published, as a single-pass scan in memory order would */
+#define FPSCAN_PROBE_ROWS8 4  /* one 512-thread workgroup per row of row_bytes, 8 KiB rounds,
+                                 two in flight (dimwise_forward; the row scans' eight-wave
+                                 rows) */
 
 #define FPSCAN_PROBE_OK 0
 #define FPSCAN_PROBE_ERR_ARG 1    /* unknown pattern or read/write count, bad size, alignment,
@@ -47,9 +50,9 @@ size_t fpscan_probe_lookback_scratch_bytes(int64_t tensor_bytes);
  * out back to back at `src` (nread * tensor_bytes bytes) and nwrite outputs back to back at
  * `dst`; (nread, nwrite) is (2, 1) -- the forward scan's traffic -- or (3, 2) -- the fused
  * backward's. tensor_bytes: a multiple of 16 KiB, at most 4 GiB; row_bytes: for
- * FPSCAN_PROBE_ROWS and FPSCAN_PROBE_BLOCKS_LOOKBACK a multiple of 16 KiB that divides
- * tensor_bytes (ignored otherwise). Pointers 16-byte aligned. Enqueued on `stream` (a
- * hipStream_t; NULL for the default stream). */
+ * FPSCAN_PROBE_ROWS, FPSCAN_PROBE_ROWS8 and FPSCAN_PROBE_BLOCKS_LOOKBACK a multiple of 16 KiB
+ * that divides tensor_bytes (ignored otherwise). Pointers 16-byte aligned. Enqueued on
+ * `stream` (a hipStream_t; NULL for the default stream). */
 int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void* dst,
                       int64_t tensor_bytes, int64_t row_bytes, void* scratch,
                       size_t scratch_bytes, void* stream);

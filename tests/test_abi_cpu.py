@@ -89,6 +89,8 @@ def test_probe_rejects_bad_arguments_before_any_launch(lib):
         (1, 2, 1, buf, buf, kib16 + 16, 0, None, 0),   # not whole tiles
         (1, 2, 1, buf, buf, (1 << 32) + kib16, 0, None, 0),  # above 4 GiB
         (2, 2, 1, buf, buf, 4 * kib16, 3 * kib16, None, 0),  # rows that do not divide
+        (4, 2, 1, buf, buf, 4 * kib16, 3 * kib16, None, 0),  # eight-wave rows likewise
+        (4, 2, 1, buf, buf, 4 * kib16, 0, None, 0),    # eight-wave rows without a row length
         (0, 2, 1, buf, buf, kib16, 0, None, 0),        # tiles without scratch
         (0, 3, 2, buf, buf, kib16, 0, buf, 64),        # scratch too small
     ]
