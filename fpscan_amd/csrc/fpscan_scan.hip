@@ -155,7 +155,9 @@ struct GatePlain {
 
 struct GateSoftplus {
   static constexpr bool kFused = true;
-  // per element, memory order: d gate / d z and d gate / d rate, for the backward
+  // per element, memory order, for the backward: from eval, rate * sigmoid(z) and softplus(z)
+  // (d gate / d z and d gate / d rate are -gate times them); make_maps then multiplies both by
+  // -gate * y[t-1]
   template <int V>
   struct Aux {
     float dz[V];
@@ -188,8 +190,8 @@ struct GateSoftplus {
     const float sp = fmaf(__builtin_amdgcn_logf(w), kLn2, zpos + sum_err);
     gate = __builtin_amdgcn_exp2f(-(sp * (rate * kLog2e)));
     const float sig = (z >= 0.0f) ? rw : t * rw;
-    dz = -gate * rate * sig;
-    dr = -gate * sp;
+    dz = rate * sig;  // d gate / d z = -gate * dz
+    dr = sp;          // d gate / d rate = -gate * dr
   }
   __device__ static __forceinline__ float gate(float z, float rate) {
     float g, dz, dr;
@@ -239,11 +241,13 @@ __device__ __forceinline__ void make_maps(const Slot<kMode>& s, float (&al)[E::V
     }
     if constexpr (Gp::kFused) {
       // d loss / d z = grad_tokens * (y[t-1] * d gate / d z), and likewise for the rate: the
-      // two products are formed here, so that y[t-1] is not held across the scan
+      // products with -gate * y[t-1] are formed here, so that neither the gate nor y[t-1] is
+      // held across the scan
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        aux->dz[e] *= ysh[V - 1 - e];
-        aux->dr[e] *= ysh[V - 1 - e];
+        const float c = -g[e] * ysh[V - 1 - e];
+        aux->dz[e] *= c;
+        aux->dr[e] *= c;
       }
     }
   } else {
