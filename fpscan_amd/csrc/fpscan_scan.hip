@@ -1000,9 +1000,9 @@ const void* long_kernel(int u) {
   // caller's choice of u): 1-3 % faster than three (fp32 B2 D256 L32768 forward 38.4 -> 37.4
   // us, fused-gate bf16 B8 D1024 L65536 556.4 -> 547.6), within 64 VGPRs; the backward at
   // four (79-97 VGPRs) measured 0.5-1 % slower than three. Other W keep at most two: their
-  // waves already multiply the bytes in flight. So does the fused-gate backward: at three it
-  // spills registers in bf16 (128 VGPRs) and measured 1-3 % slower than two in bf16 and fp32
-  // (96 and 64 VGPRs at two).
+  // waves already multiply the bytes in flight. So does the fused-gate backward: at three (126
+  // VGPRs in bf16, no spills, the same one workgroup per CU) it measured within 0.5 % of two
+  // in bf16 and fp32 at (8, 1024, 65536), (2, 512, 65536) and (4, 256, 32768).
   if constexpr (W == 16 && kMode != kBwd) {
     if (u >= 4) return reinterpret_cast<const void*>(&scan_long_rows<E, kMode, W, 4, Gp>);
   }
