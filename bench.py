@@ -28,9 +28,10 @@ p50s; ``c3`` and ``c5``: configs 3 and 5 of WORKLOADS (``--no-configs`` skips th
 
 Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen sweep, forward
 and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant), c4cl and c5cl (channel-last),
-dw (dimwise_forward), c4fused (fused softplus gates), ceiling (the library's copy probes
-with the scans' access patterns, beside the scans) and share (the B1 share object alone). Multi-GPU runs are not part
-of this build: ``--gpus N`` with N > 1 exits with a message.
+dw (dimwise_forward, beside the copy of its access pattern), c4fused (fused softplus gates),
+ceiling (the library's copy probes with the scans' access patterns, beside the scans, row and
+channel-last) and share (the B1 share object alone). Multi-GPU runs are not part of this
+build: ``--gpus N`` with N > 1 exits with a message.
 """
 from __future__ import annotations
 
