@@ -266,6 +266,12 @@ int fpscan_dimwise_fwd(const void* gates, void* tokens, const void* bh, const vo
   if (geo.W == 0) return FPSCAN_ERR_SEQLEN;
   if (batch < 0 || dim < 0) return FPSCAN_ERR_SHAPE;
   if (batch == 0 || dim == 0) return FPSCAN_OK;
+  // rows and elements checked for wrap-around; the tensors' bytes must stay below 2^48
+  // (256 TiB, far above any device memory)
+  int64_t rows = 0, elems = 0;
+  if (__builtin_mul_overflow(batch, dim, &rows) || __builtin_mul_overflow(rows, seqlen, &elems) ||
+      elems > ((int64_t)1 << 48) / 4)
+    return FPSCAN_ERR_SHAPE;
   const void* ptrs[] = {gates, tokens, bh, wq, wk};
   for (const void* p : ptrs)
     if (p == nullptr) return FPSCAN_ERR_NULL;
@@ -277,7 +283,7 @@ int fpscan_dimwise_fwd(const void* gates, void* tokens, const void* bh, const vo
       (reinterpret_cast<uintptr_t>(wq) & (size - 1)) != 0 ||
       (reinterpret_cast<uintptr_t>(wk) & (size - 1)) != 0)
     return FPSCAN_ERR_ALIGN;
-  DwArgs a{gates, tokens, bh, wq, wk, batch * dim, dim, (int32_t)seqlen, geo.W, geo.C};
+  DwArgs a{gates, tokens, bh, wq, wk, rows, dim, (int32_t)seqlen, geo.W, geo.C};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case FPSCAN_DTYPE_F32: return run_dw<F32>(a, geo.P, s);

@@ -397,10 +397,13 @@ int fpscan_probe_copy_cl(int nread, int nwrite, const void* src, void* dst, int6
   if (batch <= 0 || seqlen <= 0 || seqlen % tile_rows != 0 || row_bytes <= 0 ||
       row_bytes % strip_bytes != 0)
     return FPSCAN_PROBE_ERR_ARG;
-  const int64_t tensor_bytes = batch * seqlen * row_bytes;
-  // at most 4 GiB per tensor and a tile's range below 2 GiB (32-bit buffer offsets)
-  if (tensor_bytes > (int64_t)1 << 32 || (int64_t)tile_rows * row_bytes > INT32_MAX)
+  // at most 4 GiB per tensor (tested factor by factor, so the product cannot overflow) and a
+  // tile's range below 2 GiB (32-bit buffer offsets)
+  constexpr int64_t kMaxTensor = (int64_t)1 << 32;
+  if (row_bytes > kMaxTensor / seqlen || batch > kMaxTensor / (seqlen * row_bytes) ||
+      (int64_t)tile_rows * row_bytes > INT32_MAX)
     return FPSCAN_PROBE_ERR_ARG;
+  const int64_t tensor_bytes = batch * seqlen * row_bytes;
   const int64_t strips = row_bytes / strip_bytes;
   const int64_t nseg = seqlen / tile_rows;
   const int64_t ntiles = batch * strips * nseg;

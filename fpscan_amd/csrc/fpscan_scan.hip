@@ -1193,12 +1193,22 @@ int validate(int64_t batch, int64_t dim, int64_t seqlen, int64_t stride_b, int64
   const int size = itemsize(dtype);
   if (size == 0) return FPSCAN_ERR_DTYPE;
   if (batch < 0 || dim < 0 || stride_b < 0 || stride_d < 0) return FPSCAN_ERR_SHAPE;
+  // the row count and the element span (batch-1)*stride_b + (dim-1)*stride_d + seqlen, with
+  // every product and sum checked, so that no size the caller passes can wrap around; the
+  // span's bytes must stay below 2^48 (256 TiB, far above any device memory)
+  int64_t rows = 0, over_b = 0, over_d = 0, span = 0;
+  if (__builtin_mul_overflow(batch, dim, &rows) ||
+      __builtin_mul_overflow(batch > 0 ? batch - 1 : 0, stride_b, &over_b) ||
+      __builtin_mul_overflow(dim > 0 ? dim - 1 : 0, stride_d, &over_d) ||
+      __builtin_add_overflow(over_b, over_d, &span) ||
+      __builtin_add_overflow(span, seqlen, &span) || span > ((int64_t)1 << 48) / size)
+    return FPSCAN_ERR_SHAPE;
   if (dim > 1 && stride_d < seqlen) return FPSCAN_ERR_SHAPE;
-  if (batch > 1 && dim > 0 && stride_b < (dim - 1) * stride_d + seqlen) return FPSCAN_ERR_SHAPE;
+  if (batch > 1 && dim > 0 && stride_b < over_d + seqlen) return FPSCAN_ERR_SHAPE;
   // strides of size-1 dimensions are never used
   if (batch > 1 && ((stride_b * size) & 15) != 0) return FPSCAN_ERR_ALIGN;
   if (dim > 1 && ((stride_d * size) & 15) != 0) return FPSCAN_ERR_ALIGN;
-  a->rows = batch * dim;
+  a->rows = rows;
   a->dim = dim > 0 ? dim : 1;
   a->stride_b = stride_b;
   a->stride_d = stride_d;
@@ -1345,7 +1355,11 @@ size_t fpscan_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dt
       (seqlen & (seqlen - 1)) != 0)
     return 0;
   if (op != FPSCAN_OP_FWD && op != FPSCAN_OP_BWD) return 0;
-  const TilePlan plan = plan_tiles(batch * dim, seqlen, size,
+  int64_t rows = 0, elems = 0;
+  if (__builtin_mul_overflow(batch, dim, &rows) || __builtin_mul_overflow(rows, seqlen, &elems) ||
+      elems > ((int64_t)1 << 48) / size)
+    return 0;  // no call of this size passes validation
+  const TilePlan plan = plan_tiles(rows, seqlen, size,
                                    g_tiling.load(std::memory_order_relaxed), op == FPSCAN_OP_BWD);
   return plan.use ? plan.bytes : 0;
 }
@@ -1355,7 +1369,9 @@ const char* fpscan_strerror(int status) {
     case FPSCAN_OK: return "success";
     case FPSCAN_ERR_SEQLEN: return "seqlen must be a power of 2, >= 32, <= 65536";
     case FPSCAN_ERR_DTYPE: return "Unsupported tensor dtype: expecting bfloat16, float16 or float32";
-    case FPSCAN_ERR_SHAPE: return "invalid shape or strides: rows must not overlap";
+    case FPSCAN_ERR_SHAPE:
+      return "invalid shape or strides: rows must not overlap and a tensor must span less than "
+             "2^48 bytes";
     case FPSCAN_ERR_ALIGN: return "data pointers and row strides must be 16-byte aligned";
     case FPSCAN_ERR_NULL: return "null data pointer";
     case FPSCAN_ERR_WORKSPACE: return "workspace too small";

@@ -1101,8 +1101,14 @@ int validate_cl(int64_t batch, int64_t seqlen, int64_t dim, int64_t stride_b, in
   if (size == 0) return FPSCAN_ERR_DTYPE;
   if (batch < 0 || seqlen < 0 || dim < 0 || seqlen > INT32_MAX) return FPSCAN_ERR_SHAPE;
   if (batch == 0 || seqlen == 0 || dim == 0) return -1;  // nothing to do
-  if (stride_t < dim || stride_b < (seqlen - 1) * stride_t + dim) return FPSCAN_ERR_SHAPE;
-  if (stride_t * size > (INT32_MAX / 3)) return FPSCAN_ERR_SHAPE;
+  // stride_t is bounded first, so that (seqlen - 1) * stride_t cannot wrap around; the
+  // element span (batch-1)*stride_b + (seqlen-1)*stride_t + dim is computed with checks
+  if (stride_t < dim || stride_t > (INT32_MAX / 3) / size) return FPSCAN_ERR_SHAPE;
+  const int64_t over_t = (seqlen - 1) * stride_t;
+  int64_t over_b = 0, span = 0;
+  if (stride_b < over_t + dim || __builtin_mul_overflow(batch - 1, stride_b, &over_b) ||
+      __builtin_add_overflow(over_b, over_t + dim, &span) || span > ((int64_t)1 << 48) / size)
+    return FPSCAN_ERR_SHAPE;
   const int64_t vec = 16 / size;
   if (dim % vec != 0 || stride_t % vec != 0 || stride_b % vec != 0) return FPSCAN_ERR_ALIGN;
   for (int i = 0; i < nptrs; ++i) {
@@ -1179,6 +1185,10 @@ size_t fpscan_workspace_bytes_cl(int64_t batch, int64_t seqlen, int64_t dim, int
   if (size == 0 || batch <= 0 || seqlen <= 0 || dim <= 0 || seqlen > INT32_MAX) return 0;
   if (stride_t < dim || stride_t * size > (INT32_MAX / 3)) return 0;
   if (op != FPSCAN_OP_FWD && op != FPSCAN_OP_BWD) return 0;
+  int64_t steps = 0, elems = 0;
+  if (__builtin_mul_overflow(batch, seqlen, &steps) ||
+      __builtin_mul_overflow(steps, stride_t, &elems) || elems > ((int64_t)1 << 48) / size)
+    return 0;  // no call of this size passes validation
   const ClTilePlan tiles =
       plan_cl_tiles(batch, seqlen, dim, stride_t, size, fpscan_detail::tiling_mode());
   if (tiles.use) return tiles.bytes;

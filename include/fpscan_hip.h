@@ -73,7 +73,8 @@ extern "C" {
 #define FPSCAN_OK 0
 #define FPSCAN_ERR_SEQLEN 1    /* seqlen not a power of two in [32, 65536] */
 #define FPSCAN_ERR_DTYPE 2     /* dtype code not one of FPSCAN_DTYPE_* */
-#define FPSCAN_ERR_SHAPE 3     /* negative batch/dim/stride or rows that overlap */
+#define FPSCAN_ERR_SHAPE 3     /* negative batch/dim/stride, rows that overlap, or a tensor
+                                  span of 2^48 bytes or more */
 #define FPSCAN_ERR_ALIGN 4     /* pointer or stride not 16-byte aligned */
 #define FPSCAN_ERR_NULL 5      /* null data pointer with a non-empty problem */
 #define FPSCAN_ERR_WORKSPACE 6 /* workspace smaller than fpscan_workspace_bytes() */

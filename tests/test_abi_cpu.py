@@ -110,6 +110,7 @@ def test_probe_rejects_bad_arguments_before_any_launch(lib):
         (3, 2, buf, buf, 1, 128, 2048, 128, None, scratch),    # no scratch
         (3, 2, buf, buf, 1, 128, 2048, 128, buf, 64),          # scratch too small
         (2, 1, buf, buf, 2, 1 << 20, 4096, 128, buf, scratch),  # above 4 GiB
+        (2, 1, buf, buf, 1 << 40, 1 << 40, 1 << 40, 128, buf, scratch),  # would overflow
     ]
     for args in bad_cl:
         assert lib.fpscan_probe_copy_cl(*args, None) == 1, args
@@ -198,6 +199,14 @@ def test_bad_shape_rejected(lib):
     # rows overlapping: stride_d smaller than seqlen
     assert lib.fpscan_scan_fwd(FAKE, FAKE, FAKE, 1, 4, 64, 256, 32, 0, 0, None, 0, None) == \
         d["FPSCAN_ERR_SHAPE"]
+    # sizes whose row count or element span would wrap around a 64-bit integer, or exceed
+    # 2^48 bytes: refused, never launched
+    big = 1 << 40
+    for args in ((big, big, 64, big * 64, 64), (3, 4, 64, (1 << 62), 64),
+                 (2, big, 64, big * 64, 64), ((1 << 62), 2, 64, 128, 64)):
+        assert lib.fpscan_scan_fwd(FAKE, FAKE, FAKE, *args, 0, 0, None, 0, None) == \
+            d["FPSCAN_ERR_SHAPE"], args
+        assert lib.fpscan_workspace_bytes(args[0], args[1], args[2], 0, 0) == 0, args
 
 
 def test_misaligned_rejected(lib):
@@ -328,6 +337,11 @@ def test_channel_last_validation(cl_lib):
     assert f(None, FAKE, FAKE, 2, 100, 64, 6400, 64, 0, 0, None, 0, None) == d["FPSCAN_ERR_NULL"]
     assert f(None, None, None, 0, 100, 64, 6400, 64, 0, 0, None, 0, None) == 0  # empty
     assert f(None, None, None, 2, 0, 64, 0, 64, 0, 0, None, 0, None) == 0
+    # spans that would wrap around a 64-bit integer or exceed 2^48 bytes
+    assert f(FAKE, FAKE, FAKE, 1 << 40, 1 << 30, 64, 64 << 30, 64, 0, 0, None, 0, None) == \
+        d["FPSCAN_ERR_SHAPE"]
+    assert f(FAKE, FAKE, FAKE, 3, 100, 64, 1 << 62, 64, 0, 0, None, 0, None) == \
+        d["FPSCAN_ERR_SHAPE"]
     b = cl_lib.fpscan_scan_bwd_cl
     assert b(FAKE, FAKE, FAKE, FAKE, None, 2, 100, 64, 6400, 64, 0, None, 0, None) == \
         d["FPSCAN_ERR_NULL"]
@@ -412,6 +426,7 @@ def test_dimwise_groups_and_validation(lib):
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 32, 0, None) == d["FPSCAN_ERR_SEQLEN"]
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 64, 3, None) == d["FPSCAN_ERR_DTYPE"]
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, -1, 4, 64, 0, None) == d["FPSCAN_ERR_SHAPE"]
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 40, 1 << 40, 64, 0, None) == d["FPSCAN_ERR_SHAPE"]
     assert f(FAKE, None, FAKE, FAKE, FAKE, 2, 4, 64, 0, None) == d["FPSCAN_ERR_NULL"]
     assert f(FAKE + 4, FAKE, FAKE, FAKE, FAKE, 2, 4, 64, 0, None) == d["FPSCAN_ERR_ALIGN"]
     assert f(None, None, None, None, None, 0, 4, 64, 0, None) == 0  # empty
