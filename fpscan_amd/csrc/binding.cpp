@@ -310,9 +310,12 @@ void dimwise_forward(const at::Tensor& Ax, const at::Tensor& Bx, const at::Tenso
 
   c10::hip::HIPGuardMasqueradingAsCUDA guard(Bx.device());
   void* stream = launch_stream(Bx);
-  const int status = fpscan_dimwise_fwd(Ax.data_ptr(), Bx.data_ptr(), Bh.data_ptr(),
-                                        Wq.data_ptr(), Wk.data_ptr(), B, D, L,
-                                        dtype_code(Bx.scalar_type()), stream);
+  const int dt = dtype_code(Bx.scalar_type());
+  const size_t ws_bytes = fpscan_dimwise_workspace_bytes(B, D, L, dt);
+  at::Tensor ws = workspace(ws_bytes, Bx);
+  const int status = fpscan_dimwise_fwd_ws(Ax.data_ptr(), Bx.data_ptr(), Bh.data_ptr(),
+                                           Wq.data_ptr(), Wk.data_ptr(), B, D, L, dt,
+                                           ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
   check_status(status);
 }
 
@@ -433,6 +436,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("dimwise_groups", &fpscan_dimwise_groups,
         "Bh entries per row expected by dimwise_forward for this seqlen (0: unsupported)",
         pybind11::arg("seqlen"));
+  m.def("dimwise_workspace_bytes", &fpscan_dimwise_workspace_bytes,
+        "workspace dimwise_forward allocates for its tiled path (0: it takes the row kernel)",
+        pybind11::arg("batch"), pybind11::arg("dim"), pybind11::arg("seqlen"),
+        pybind11::arg("dtype"));
   m.def("set_launch_override", &set_launch_override,
         "tuning hook: force waves per row / ring depth (0 = built-in choice)",
         pybind11::arg("waves_per_row"), pybind11::arg("ring_depth"));

@@ -14,7 +14,9 @@
 //   ROWS    one 1024-thread workgroup per row of `row_bytes`, walked in 16 KiB rounds with four
 //           rounds in flight (the pattern of the row-streaming scan with 16 waves per row).
 //   ROWS8   one 512-thread workgroup per row, 8 KiB rounds, two in flight (the pattern of
-//           dimwise_forward and of the row scans with eight waves per row).
+//           dimwise_forward's row kernel and of the row scans with eight waves per row).
+//   TILES8  as TILES with 8 KiB tiles and 512-thread workgroups, two per CU (the pattern of
+//           dimwise_forward's tiled path for 2-byte types).
 //   BLOCKS_LOOKBACK  256-thread blocks of 16 KiB tiles in memory order, each waiting before its
 //           stores until every earlier tile of its row has loaded its data: the wait a
 //           single-pass scan in memory order needs.
@@ -49,14 +51,15 @@ __device__ __forceinline__ void combine_store(const u32x4 (&v)[NR], const Rsrc (
 
 // Tile geometries of probe_tiles: the claim groups, where a tile lies in a tensor and this
 // lane's byte offset in it.
-// Row tiles: 16 KiB contiguous, groups of contiguous eighths.
+// Row tiles: TB bytes contiguous (one 16-byte vector per lane), groups of contiguous eighths.
+template <int TB>
 struct RowTileGeo {
   int64_t ntiles;
   __device__ RowGroups groups() const { return RowGroups{ntiles, 0}; }
   __device__ uint32_t lane_off() const { return threadIdx.x * 16u; }
   __device__ Rsrc rsrc(const char* base, int64_t t) const {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + t * kTileBytes, (short)0,
-                                             kTileBytes, kRsrcWord3);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + t * TB, (short)0, TB,
+                                             kRsrcWord3);
   }
 };
 
@@ -106,8 +109,8 @@ struct ClTileGeo {
   }
 };
 
-template <int NR, int NW, class Geo>
-__global__ void __launch_bounds__(1024)
+template <int NR, int NW, class Geo, int THREADS>
+__global__ void __launch_bounds__(THREADS)
 probe_tiles(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_bytes,
             uint64_t* __restrict__ status, int64_t ntiles, const Geo geo) {
   const bool leader = threadIdx.x == 0;
@@ -285,9 +288,9 @@ probe_rows(const char* __restrict__ src, char* __restrict__ dst, int64_t tensor_
   }
 }
 
-// The persistent grid of probe_tiles over `geo`: one workgroup per resident slot, after a
-// clear of the claim counters on the same stream.
-template <int NR, int NW, class Geo>
+// The persistent grid of probe_tiles over `geo`: one workgroup of THREADS per resident slot,
+// after a clear of the claim counters on the same stream.
+template <int NR, int NW, class Geo, int THREADS = 1024>
 int launch_tiles(const char* s, char* d, int64_t tensor_bytes, int64_t ntiles, const Geo& geo,
                  void* scratch, hipStream_t stream) {
   uint64_t* status = static_cast<uint64_t*>(scratch);
@@ -297,13 +300,13 @@ int launch_tiles(const char* s, char* d, int64_t tensor_bytes, int64_t ntiles, c
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu, reinterpret_cast<const void*>(&probe_tiles<NR, NW, Geo>), 1024, 0) !=
-          hipSuccess ||
+          &per_cu, reinterpret_cast<const void*>(&probe_tiles<NR, NW, Geo, THREADS>), THREADS,
+          0) != hipSuccess ||
       cus <= 0 || per_cu <= 0)
     return FPSCAN_PROBE_ERR_DEVICE;
   const int64_t grid = (int64_t)cus * per_cu < ntiles ? (int64_t)cus * per_cu : ntiles;
-  hipLaunchKernelGGL((probe_tiles<NR, NW, Geo>), dim3((unsigned)grid), dim3(1024), 0, stream, s,
-                     d, tensor_bytes, status, ntiles, geo);
+  hipLaunchKernelGGL((probe_tiles<NR, NW, Geo, THREADS>), dim3((unsigned)grid), dim3(THREADS), 0,
+                     stream, s, d, tensor_bytes, status, ntiles, geo);
   return hipGetLastError() == hipSuccess ? FPSCAN_PROBE_OK : FPSCAN_PROBE_ERR_LAUNCH;
 }
 
@@ -330,9 +333,14 @@ int launch_probe(int pattern, const void* src, void* dst, int64_t tensor_bytes, 
   } else if (pattern == FPSCAN_PROBE_ROWS8) {
     hipLaunchKernelGGL((probe_rows<NR, NW, 8, 2>), dim3((unsigned)(tensor_bytes / row_bytes)),
                        dim3(512), 0, stream, s, d, tensor_bytes, row_bytes);
+  } else if (pattern == FPSCAN_PROBE_TILES8) {
+    const int64_t ntiles = tensor_bytes / (kTileBytes / 2);
+    return launch_tiles<NR, NW, RowTileGeo<kTileBytes / 2>, 512>(
+        s, d, tensor_bytes, ntiles, RowTileGeo<kTileBytes / 2>{ntiles}, scratch, stream);
   } else {
     const int64_t ntiles = tensor_bytes / kTileBytes;
-    return launch_tiles<NR, NW>(s, d, tensor_bytes, ntiles, RowTileGeo{ntiles}, scratch, stream);
+    return launch_tiles<NR, NW>(s, d, tensor_bytes, ntiles, RowTileGeo<kTileBytes>{ntiles},
+                                scratch, stream);
   }
   return hipGetLastError() == hipSuccess ? FPSCAN_PROBE_OK : FPSCAN_PROBE_ERR_LAUNCH;
 }
@@ -352,7 +360,7 @@ int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void*
                       size_t scratch_bytes, void* stream) {
   if (pattern != FPSCAN_PROBE_TILES && pattern != FPSCAN_PROBE_BLOCKS &&
       pattern != FPSCAN_PROBE_ROWS && pattern != FPSCAN_PROBE_BLOCKS_LOOKBACK &&
-      pattern != FPSCAN_PROBE_ROWS8)
+      pattern != FPSCAN_PROBE_ROWS8 && pattern != FPSCAN_PROBE_TILES8)
     return FPSCAN_PROBE_ERR_ARG;
   if (!((nread == 2 && nwrite == 1) || (nread == 3 && nwrite == 2))) return FPSCAN_PROBE_ERR_ARG;
   if (src == nullptr || dst == nullptr) return FPSCAN_PROBE_ERR_ARG;
@@ -371,10 +379,9 @@ int fpscan_probe_copy(int pattern, int nread, int nwrite, const void* src, void*
        (reinterpret_cast<uintptr_t>(scratch) & 3u) != 0 ||
        scratch_bytes < fpscan_probe_lookback_scratch_bytes(tensor_bytes)))
     return FPSCAN_PROBE_ERR_ARG;
-  if (pattern == FPSCAN_PROBE_TILES &&
+  if ((pattern == FPSCAN_PROBE_TILES || pattern == FPSCAN_PROBE_TILES8) &&
       (scratch == nullptr || scratch_bytes < fpscan_probe_scratch_bytes() ||
-       (reinterpret_cast<uintptr_t>(scratch) & 7u) != 0 ||
-       tensor_bytes / kTileBytes > (int64_t)UINT32_MAX))
+       (reinterpret_cast<uintptr_t>(scratch) & 7u) != 0))
     return FPSCAN_PROBE_ERR_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return nread == 2 ? launch_probe<2, 1>(pattern, src, dst, tensor_bytes, row_bytes, scratch, s)

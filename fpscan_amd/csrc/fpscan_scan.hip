@@ -1221,7 +1221,7 @@ int validate(int64_t batch, int64_t dim, int64_t seqlen, int64_t stride_b, int64
 }  // namespace
 
 // Path selection set by fpscan_set_tiling and the look-back test hook, read by the
-// channel-last launcher as well; the channel-last counter of given-up waits.
+// channel-last and dimwise launchers as well; their counters of given-up waits.
 namespace fpscan_detail {
 int tiling_mode() { return g_tiling.load(std::memory_order_relaxed); }
 int64_t hook_skip_publish() { return g_hook_skip_publish.load(std::memory_order_relaxed); }
@@ -1230,6 +1230,7 @@ int hook_spin_limit() {
   return spin > 0 ? spin : kSpinLimit;
 }
 int cl_overruns(unsigned long long* count);  // fpscan_scan_cl.hip
+int dw_overruns(unsigned long long* count);  // fpscan_dimwise.hip
 }  // namespace fpscan_detail
 
 namespace fpscan_detail {
@@ -1387,12 +1388,14 @@ const char* fpscan_strerror(int status) {
 int fpscan_lookback_overruns(unsigned long long* count) {
   if (count == nullptr) return FPSCAN_ERR_NULL;
   if (hipDeviceSynchronize() != hipSuccess) return FPSCAN_ERR_DEVICE;
-  unsigned long long rows = 0, cl = 0;
+  unsigned long long rows = 0, cl = 0, dw = 0;
   int st = fpscan_detail::row_overruns(&rows);
   if (st != FPSCAN_OK) return st;
   st = fpscan_detail::cl_overruns(&cl);
   if (st != FPSCAN_OK) return st;
-  *count = rows + cl;
+  st = fpscan_detail::dw_overruns(&dw);
+  if (st != FPSCAN_OK) return st;
+  *count = rows + cl + dw;
   return FPSCAN_OK;
 }
 

@@ -207,10 +207,30 @@ int fpscan_scan_bwd_softplus(const void* z, const float* rate, const void* out,
  * a first-maximum selection of (1+Wk)*Bh[h] * (1+Wq)*v[g] over earlier groups h. fp32
  * arithmetic with one rounding, except the selection's k, q and scores, which are rounded as
  * the reference rounds them in the tensors' type. Runs on `stream` (the reference uses the
- * legacy default stream). No workspace, no backward (the reference has none). */
+ * legacy default stream). No backward (the reference has none). Takes the row kernel (one
+ * workgroup per row); fpscan_dimwise_fwd_ws with a workspace can take the faster tiled path. */
 int fpscan_dimwise_fwd(const void* gates, void* tokens, const void* bh, const void* wq,
                        const void* wk, int64_t batch, int64_t dim, int64_t seqlen, int dtype,
                        void* stream);
+
+/* fpscan_dimwise_fwd with a workspace: problems of at least 512 MiB per tensor with seqlen
+ * 8192..65536 (every chunk 32 groups of 128) then take a tiled path, whose 16 KiB tiles are
+ * claimed in memory order and chained by a look-back over the chunks' carry maps (the carry
+ * enters a chunk affinely: only group 0 depends on it, and the selection does not), with
+ * bounded waits as the tiled scans'. It needs fpscan_dimwise_workspace_bytes() bytes, 8-byte
+ * aligned, owned by the caller and not used by any call in flight; with no workspace or a
+ * smaller one the call takes the row kernel. Same results up to fp32 rounding order, except
+ * where the selection finds no score above the initial one (non-finite or |score| >= 1e10
+ * inputs): the non-finite outputs may then differ in kind. fpscan_set_tiling applies (1: row
+ * kernel only; 2: tiled for any seqlen of 8192 or more). The reference's dimwise_forward takes
+ * no workspace: the torch binding allocates it from the caching allocator. */
+int fpscan_dimwise_fwd_ws(const void* gates, void* tokens, const void* bh, const void* wq,
+                          const void* wk, int64_t batch, int64_t dim, int64_t seqlen, int dtype,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace, in bytes, that fpscan_dimwise_fwd_ws uses for this problem (0: it takes the row
+ * kernel, or the arguments are invalid). No reference counterpart. */
+size_t fpscan_dimwise_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int dtype);
 
 /* Number of Bh entries per row (G = W * C) that fpscan_dimwise_fwd expects for this seqlen,
  * 0 if seqlen is not supported. Only the first W (<= 32) are read: the reference indexes Bh
@@ -224,7 +244,7 @@ const char* fpscan_strerror(int status);
 /* FPSCAN_ABI_VERSION of the loaded library. */
 int fpscan_abi_version(void);
 
-/* Look-back waits (row and channel-last tiled kernels) that gave up on the current device
+/* Look-back waits (row, channel-last and dimwise tiled kernels) that gave up on the current device
  * since the library was loaded; 0 in a correct run. Waits for all work on the device first
  * (hipDeviceSynchronize), then copies the device counters. No reference counterpart: the
  * reference keeps every carry inside one block (full_scan.cu:77-175) and has no such wait. */

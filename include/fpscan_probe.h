@@ -26,18 +26,20 @@ extern "C" {
                                  (bounded) until every earlier tile of its row of row_bytes
                                  has published, as a single-pass scan in memory order would */
 #define FPSCAN_PROBE_ROWS8 4  /* one 512-thread workgroup per row of row_bytes, 8 KiB rounds,
-                                 two in flight (dimwise_forward; the row scans' eight-wave
-                                 rows) */
+                                 two in flight (dimwise_forward's row kernel; the row scans'
+                                 eight-wave rows) */
+#define FPSCAN_PROBE_TILES8 5 /* as FPSCAN_PROBE_TILES with 8 KiB tiles and 512-thread
+                                 workgroups (dimwise_forward's tiled path, 2-byte types) */
 
 #define FPSCAN_PROBE_OK 0
 #define FPSCAN_PROBE_ERR_ARG 1    /* unknown pattern or read/write count, bad size, alignment,
-                                     or a missing scratch buffer for FPSCAN_PROBE_TILES */
+                                     or a missing scratch buffer for the tile patterns */
 #define FPSCAN_PROBE_ERR_LAUNCH 2 /* the launch failed */
 #define FPSCAN_PROBE_ERR_DEVICE 3 /* the current device or the kernel's occupancy could not be
                                      queried */
 
-/* Bytes of device scratch FPSCAN_PROBE_TILES needs for its claim counters (cleared by the
- * call, on the stream, before the copy). */
+/* Bytes of device scratch FPSCAN_PROBE_TILES and FPSCAN_PROBE_TILES8 need for their claim
+ * counters (cleared by the call, on the stream, before the copy). */
 size_t fpscan_probe_scratch_bytes(void);
 
 /* Bytes of device scratch FPSCAN_PROBE_BLOCKS_LOOKBACK needs for tensors of tensor_bytes: two

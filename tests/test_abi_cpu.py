@@ -430,3 +430,46 @@ def test_dimwise_groups_and_validation(lib):
     assert f(FAKE, None, FAKE, FAKE, FAKE, 2, 4, 64, 0, None) == d["FPSCAN_ERR_NULL"]
     assert f(FAKE + 4, FAKE, FAKE, FAKE, FAKE, 2, 4, 64, 0, None) == d["FPSCAN_ERR_ALIGN"]
     assert f(None, None, None, None, None, 0, 4, 64, 0, None) == 0  # empty
+
+
+def test_dimwise_workspace_and_validation(lib):
+    """fpscan_dimwise_workspace_bytes: one status word per 16 KiB tile (two chunks of 4096
+    elements of a 2-byte type, one of fp32) plus the counters when the tiled path is taken
+    (seqlen >= 8192, tensors below 4 GiB; automatically from 512 MiB per tensor), else 0;
+    fpscan_dimwise_fwd_ws validates like fpscan_dimwise_fwd and checks the workspace's
+    alignment before any launch."""
+    d = header_defines()
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    wb = lib.fpscan_dimwise_workspace_bytes
+    wb.argtypes = [i64, i64, i64, ctypes.c_int]
+    wb.restype = ctypes.c_size_t
+    lib.fpscan_set_tiling.argtypes = [ctypes.c_int]
+    extra = 16 * 9  # overrun word and claim counters, as the row scan's
+    try:
+        assert wb(8, 1024, 65536, 2) == (8192 * 8 + extra) * 8    # bf16: 8 tiles per row
+        assert wb(8, 1024, 65536, 0) == (8192 * 16 + extra) * 8   # fp32: 16
+        assert wb(16, 1024, 65536, 0) == 0                         # 4 GiB: row kernel
+        assert wb(1, 1024, 65536, 2) == 0                          # 128 MiB: row kernel
+        assert wb(8, 1024, 4096, 2) == 0                           # one chunk per row
+        for bad in [(8, 1024, 65536, 3), (8, 1024, 96, 2), (-1, 4, 65536, 2),
+                    (1 << 40, 1 << 40, 65536, 2)]:
+            assert wb(*bad) == 0, bad
+        assert lib.fpscan_set_tiling(2) == 0
+        assert wb(2, 4, 8192, 2) == (8 + extra) * 8                # one tile per row
+        assert wb(2, 4, 8192, 0) == (16 + extra) * 8               # fp32: two
+        assert wb(2, 4, 4096, 2) == 0
+        assert lib.fpscan_set_tiling(1) == 0
+        assert wb(8, 1024, 65536, 2) == 0
+    finally:
+        lib.fpscan_set_tiling(0)
+    f = lib.fpscan_dimwise_fwd_ws
+    f.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_int, vp, ctypes.c_size_t, vp]
+    ws = 1 << 20
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 32, 0, FAKE, ws, None) == d["FPSCAN_ERR_SEQLEN"]
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 8192, 3, FAKE, ws, None) == d["FPSCAN_ERR_DTYPE"]
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 40, 1 << 40, 8192, 0, FAKE, ws,
+             None) == d["FPSCAN_ERR_SHAPE"]
+    assert f(FAKE, FAKE, None, FAKE, FAKE, 2, 4, 8192, 0, FAKE, ws, None) == d["FPSCAN_ERR_NULL"]
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 8192, 0, FAKE + 4, ws,
+             None) == d["FPSCAN_ERR_ALIGN"]
+    assert f(None, None, None, None, None, 0, 4, 8192, 0, None, 0, None) == 0  # empty

@@ -14,6 +14,7 @@ import torch
 
 import fpscan_amd
 import oracle
+from fpscan_amd import ops
 from scan_helpers import DEVICE, DTYPES, check
 
 pytestmark = [
@@ -22,6 +23,22 @@ pytestmark = [
 ]
 
 SEQLENS = sorted(oracle.DIMWISE_GEOMETRY)
+# seqlens with two or more chunks of 32 groups of 128, where the tiled path applies
+TILED_SEQLENS = [L for L in SEQLENS if L >= 8192]
+
+
+class tiling:
+    """Path selection for the duration of a block: 1 row kernel only, 2 tiled when the
+    seqlen allows (fpscan_set_tiling)."""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        ops.set_tiling(self.mode)
+
+    def __exit__(self, *exc):
+        ops.set_tiling(0)
 
 
 def driver_inputs(B, D, L, seed=0):
@@ -138,9 +155,64 @@ def test_empty_and_validation():
     assert fpscan_amd.dimwise_groups(65536) == 512 and fpscan_amd.dimwise_groups(32) == 0
 
 
+# ------------------------------------------------------------------ tiled path
+@pytest.mark.parametrize("L", TILED_SEQLENS)
+def test_tiled_fp32_driver_distribution_matches_oracle(L):
+    with tiling(2):
+        got, want = run(*driver_inputs(2, 4, L, seed=L), torch.float32)
+    check(got, want, torch.float32, f"dimwise tiled fp32 L{L}")
+    assert np.abs(got.double().cpu().numpy() - want).max() < 1e-3
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("L", TILED_SEQLENS)
+@pytest.mark.parametrize("sign", [1.0, -1.0], ids=["q>0", "q<0"])
+def test_tiled_separated_keys_match_oracle(L, dtype, sign):
+    with tiling(2):
+        got, want = run(*separated_inputs(2, 3, L, sign=sign, seed=L + 7), dtype)
+    check(got, want, dtype, f"dimwise tiled {dtype} L{L} sign {sign}")
+
+
+@pytest.mark.parametrize("L", [8192, 16384, 65536])
+def test_tiled_unit_gates_zero_keys_exact(L):
+    """As test_unit_gates_zero_keys_exact on the tiled path: the carry maps composed across
+    tiles are exact on integers too, so the output equals the oracle bit for bit."""
+    W, P, C = oracle.DIMWISE_GEOMETRY[L]
+    gen = torch.Generator().manual_seed(L + 1)
+    x = torch.randint(-4, 5, (2, 3, L), generator=gen).float()
+    ones = torch.ones_like(x)
+    with tiling(2):
+        got, want = run(ones, x, torch.zeros(2, 3, W * C), torch.zeros(3), torch.zeros(3),
+                        torch.float32)
+    assert torch.equal(got.cpu().double(), torch.from_numpy(want))
+
+
+def test_tiled_first_gate_is_ignored():
+    ax, bx, bh, wq, wk = driver_inputs(1, 2, 16384, seed=4)
+    axn = ax.clone()
+    axn[:, :, 0] = float("nan")
+    with tiling(2):
+        got, _ = run(axn, bx, bh, wq, wk, torch.float32)
+        ref, _ = run(ax, bx, bh, wq, wk, torch.float32)
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("L", [8192, 32768])
+def test_tiled_shapes_and_rows(L):
+    """Ragged row counts and a single row; at 8192 a bf16 row is one tile (no look-back),
+    an fp32 row two."""
+    for B, D in [(1, 1), (3, 5), (7, 33)]:
+        for dtype in (torch.float32, torch.bfloat16):
+            with tiling(2):
+                got, want = run(*separated_inputs(B, D, L, seed=B * D + L), dtype)
+            check(got, want, dtype, f"dimwise tiled {dtype} B{B} D{D} L{L}")
+
+
+@pytest.mark.parametrize("mode", [1, 2], ids=["rows", "tiled"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
-def test_headline_shape_b8_d1024_l65536(dtype):
-    """The headline shape: sampled rows against the oracle (all rows run on the GPU)."""
+def test_headline_shape_b8_d1024_l65536(dtype, mode):
+    """The headline shape on each path: sampled rows against the oracle (all rows run on the
+    GPU)."""
     gen = torch.Generator(device=DEVICE).manual_seed(11)
     B, D, L = 8, 1024, 65536
     ax = (0.99 + 0.01 * torch.rand(B, D, L, generator=gen, device=DEVICE)).to(dtype)
@@ -155,5 +227,8 @@ def test_headline_shape_b8_d1024_l65536(dtype):
     sel = lambda t: t.reshape(B * D, -1)[rows].reshape(1, len(rows), -1).cpu()  # noqa: E731
     want = oracle.dimwise_f64(sel(ax), sel(bx), sel(bh), wq.cpu()[[r % D for r in rows]],
                               wk.cpu()[[r % D for r in rows]])
-    fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk)
-    check(sel(bx), want, dtype, f"dimwise headline {dtype}")
+    before = fpscan_amd.lookback_overruns()
+    with tiling(mode):
+        fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk)
+    check(sel(bx), want, dtype, f"dimwise headline {dtype} tiling {mode}")
+    assert fpscan_amd.lookback_overruns() == before

@@ -386,3 +386,42 @@ def test_graph_capture_is_refused_before_any_launch():
         y = fpscan_amd.scan_forward(g, x)
     torch.cuda.synchronize()
     assert bits_equal(y, fpscan_amd.scan_forward(g, x))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_dimwise_overrun_poisons_and_is_counted(dtype):
+    """dimwise_forward's tiled path: 3 rows of 4 tiles; tile 1 (row 0, second tile) never
+    publishes its map, so tiles 2 and 3 of row 0 give up waiting. Their carry is NaN: group 0
+    of each of their chunks (which continues from the carry) must be NaN, every other element
+    of them NaN or equal to an unhooked run (a group whose r does not go through group 0 is
+    independent of the carry), and everything outside them equal to the unhooked run; the
+    device counter grows by the waits that gave up."""
+    tile_len = 8192 if dtype == torch.bfloat16 else 4096  # 16 KiB
+    L = 4 * tile_len
+    gen = torch.Generator().manual_seed(13)
+    G = fpscan_amd.dimwise_groups(L)
+    ax = 0.99 + 0.01 * torch.rand(1, 3, L, generator=gen)
+    bx = torch.randn(1, 3, L, generator=gen) / G
+    bh = torch.randn(1, 3, G, generator=gen) / G
+    wq, wk = 0.01 * torch.rand(3, generator=gen), 0.01 * torch.rand(3, generator=gen)
+    t = [v.to(dtype).to(DEVICE) for v in (ax, bx, bh, wq, wk)]
+    with tiling(2):
+        want = t[1].clone()
+        fpscan_amd.dimwise_forward(t[0], want, *t[2:])
+        before = fpscan_amd.lookback_overruns()
+        with lookback_hook(1):
+            got = t[1].clone()
+            fpscan_amd.dimwise_forward(t[0], got, *t[2:])
+            torch.cuda.synchronize()
+        after = fpscan_amd.lookback_overruns()
+    assert after - before >= 2, f"given-up waits not counted ({before} -> {after})"
+    got, want = got.cpu(), want.cpu()
+    hit = torch.zeros(got.shape, dtype=torch.bool)
+    hit[0, 0, 2 * tile_len:] = True
+    assert torch.equal(got[~hit], want[~hit]), "tiles that waited normally changed"
+    g, w = got[0, 0, 2 * tile_len:], want[0, 0, 2 * tile_len:]
+    assert (torch.isnan(g) | (g == w)).all(), "a value that is neither NaN nor the unhooked one"
+    group0 = g.view(-1, 4096)[:, :128]
+    assert torch.isnan(group0).all(), "group 0 of a tile whose wait gave up must be NaN"
+    with pytest.raises(RuntimeError, match="gave up"):
+        fpscan_amd.check_lookback()
