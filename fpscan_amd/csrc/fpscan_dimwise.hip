@@ -340,9 +340,12 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
   constexpr int kTileGroups = kChunks * kDwW;  // (chunk, group) pairs of a tile
   constexpr int kSelWaves = DwGeo<E>::kSelWaves;
   constexpr int kSelSpan = DwGeo<E>::kSelSpan;
-  static_assert(kSelWaves * kSelSpan == kDwW && kSelWaves <= TW, "every candidate tested");
+  static_assert(kSelWaves * kSelSpan == kDwW && kSelWaves < TW, "every candidate tested");
+  // the first wave after the selection waves runs the look-back and makes the claims, at
+  // the same time as the selection
+  constexpr int kLookWave = kSelWaves;
 
-  __shared__ float v_lds[kTileGroups];                 // zero-carry group ends, tile reduced now
+  __shared__ float v_lds[2][kTileGroups];  // zero-carry group ends, by step parity
   __shared__ f32x2 part_lds[kSelWaves][kTileGroups];   // partial selections: (best, m as bits)
   __shared__ f32x2 sel_lds[N][kTileGroups];  // per ring slot: r[g](c) = via0 ? x v0(c) + y : y
   __shared__ uint64_t via0_lds[N];           // per ring slot: groups whose r goes through v0
@@ -372,7 +375,7 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
 #pragma unroll
   for (int i = 0; i < N; ++i) pending[i] = Claim{0, 0};
   bool claims_done = false;
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 64 * kLookWave) {
     const int64_t t0 = claims.next_now(st, kBubble, kDone);
     const int64_t t1 = (t0 == kDone) ? kDone : claims.next_now(st, kBubble, kDone);
     first_tiles[0] = t0;
@@ -387,7 +390,7 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     held_word = status_load(st, kNoOffset);
-    pending[N - 2 + i] = claims.issue(st, threadIdx.x == 0 && !claims_done);
+    pending[N - 2 + i] = claims.issue(st, threadIdx.x == 64 * kLookWave && !claims_done);
     dw_setup<E, TW>(a, tax, tbx, ring[i],
                     min(__builtin_amdgcn_readfirstlane(first_tiles[i]), ntiles), ntiles, tpr_log2,
                     w, lane0);
@@ -415,7 +418,7 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
     // a compare, instead of across the loop in scalar registers that the compiler spills
     int lane = lane0;
     asm volatile("" : "+v"(lane));
-    const bool leader = w == 0 && lane == 0;
+    const bool leader = w == kLookWave && lane == 0;
     const int ch = w / kWavesPerChunk;                               // this lane's chunk
     const int g = (w % kWavesPerChunk) * kGroupsPerWave + lane / GL;  // its group in it
     const int sl = lane % GL;
@@ -443,7 +446,7 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
     }
     segment_scan<GL>(A, B, sl);
     if (sl == GL - 1) {
-      v_lds[ch * kDwW + g] = B;
+      v_lds[u % 2][ch * kDwW + g] = B;
       if (g == 0) g0_lds[u][ch] = f32x2{A, B};
     }
     lds_barrier();
@@ -460,7 +463,7 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
       const float wk = widen_par<E>((uint32_t)__builtin_amdgcn_readlane((int)cur.par, kDwW + 1));
       const float wq = widen_par<E>((uint32_t)__builtin_amdgcn_readlane((int)cur.par, kDwW));
       const float k = scale1p<E>(wk, widen_par<E>(cur.par));  // lanes j < kSelSpan: k[h]
-      const float q = scale1p<E>(wq, round_t<E>(v_lds[pair]));
+      const float q = scale1p<E>(wq, round_t<E>(v_lds[u % 2][pair]));
       float best = kInit;
       int mi = 0;
       int t = sg - h0;  // candidate i passes h < g iff i < t
@@ -490,60 +493,10 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
       }
       if (lane < kTileGroups) part_lds[w][pair] = f32x2{best, __int_as_float(m)};
     }
-    lds_barrier();
 
-    // (3a) wave 1: a group's selection is the first of the partial maxima that exceeds the
-    // ones before it (ties keep the earlier h, as one pass over h does); then the terms r[g]
-    // for the finish and the tile's carry map, published at once
-    if (w == kDwSelWave) {
-      const int pair = lane % kTileGroups;
-      const int sg = pair % kDwW, sc = pair / kDwW;
-      f32x2 pm = part_lds[0][pair];
-      float best = pm.x;
-      int m = __float_as_int(pm.y);
-#pragma unroll
-      for (int i = 1; i < kSelWaves; ++i) {
-        pm = part_lds[i][pair];
-        if (pm.x > best) {
-          best = pm.x;
-          m = __float_as_int(pm.y);
-        }
-      }
-      const float vg = v_lds[pair];
-      // r[0] = v0(c); r[g] = best v0(c) + v[g] when m = 0; else the constant best v[m] + v[g]
-      const bool via0 = sg == 0 || m == 0;
-      const float x = sg == 0 ? 1.0f : best;
-      const float y = sg == 0 ? 0.0f : (m == 0 ? vg : fmaf(best, v_lds[sc * kDwW + m], vg));
-      if (lane < kTileGroups) sel_lds[u][pair] = f32x2{x, y};
-      const uint64_t via0_mask = __builtin_amdgcn_ballot_w64(via0);
-      if (lane == 0) via0_lds[u] = via0_mask;
-      // each chunk's carry map v[W-1] + r[W-2](c) = A c + B, composed over the tile's chunks
-      float tA = 1.0f, tB = 0.0f;
-#pragma unroll
-      for (int cc = 0; cc < kChunks; ++cc) {
-        const int l = cc * kDwW + kDwW - 2;
-        const float x30 = readlane(x, l), y30 = readlane(y, l), v31 = readlane(vg, l + 1);
-        const f32x2 g0 = g0_lds[u][cc];
-        const bool f30 = ((via0_mask >> l) & 1) != 0;
-        const float mA = f30 ? x30 * g0.x : 0.0f;
-        const float mB = v31 + (f30 ? fmaf(x30, g0.y, y30) : y30);
-        if (cc == 0) {
-          if (lane == 0) map_lds[u] = f32x2{mA, mB};
-          tA = mA;
-          tB = mB;
-        } else {
-          tB = fmaf(mA, tB, mB);
-          tA = mA * tA;
-        }
-      }
-      const bool publisher = cur_live && lane == 0 && cur.tile != a.skip_publish;
-      status_store(st, publisher ? (uint32_t)(cur.tile * sizeof(uint64_t)) : kNoOffset,
-                   pack_map(tA, tB));
-    }
-
-    // (3b) wave 0: the finishing tile's carry from its predecessor words (loaded right after
-    // the previous step's finish)
-    if (w == 0) {
+    // (3) the look-back wave, meanwhile: the finishing tile's carry from its predecessor
+    // words (loaded right after the previous step's finish), and the claim resolved
+    if (w == kLookWave) {
       uint64_t word = held_word;
       if (__builtin_amdgcn_ballot_w64(word == kNotPublished) != 0) {
         // a predecessor was not published yet: poll (bounded), with an atomic load that the
@@ -585,7 +538,57 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
     all_claimed = claim == kDone;
     const int64_t refill = claim < ntiles ? claim : ntiles;
 
-    // (4) finish the oldest deferred tile (nothing is stored while the ring fills)
+    // (4) wave 1: a group's selection is the first of the partial maxima that exceeds the
+    // ones before it (ties keep the earlier h, as one pass over h does); then the terms r[g]
+    // for the tile's finish and its carry map, published at once. Off the other waves'
+    // path: they go on to finish the deferred tile, whose terms were made D steps ago.
+    if (w == kDwSelWave) {
+      const int pair = lane % kTileGroups;
+      const int sg = pair % kDwW, sc = pair / kDwW;
+      f32x2 pm = part_lds[0][pair];
+      float best = pm.x;
+      int m = __float_as_int(pm.y);
+#pragma unroll
+      for (int i = 1; i < kSelWaves; ++i) {
+        pm = part_lds[i][pair];
+        if (pm.x > best) {
+          best = pm.x;
+          m = __float_as_int(pm.y);
+        }
+      }
+      const float vg = v_lds[u % 2][pair];
+      // r[0] = v0(c); r[g] = best v0(c) + v[g] when m = 0; else the constant best v[m] + v[g]
+      const bool via0 = sg == 0 || m == 0;
+      const float x = sg == 0 ? 1.0f : best;
+      const float y = sg == 0 ? 0.0f : (m == 0 ? vg : fmaf(best, v_lds[u % 2][sc * kDwW + m], vg));
+      if (lane < kTileGroups) sel_lds[u][pair] = f32x2{x, y};
+      const uint64_t via0_mask = __builtin_amdgcn_ballot_w64(via0);
+      if (lane == 0) via0_lds[u] = via0_mask;
+      // each chunk's carry map v[W-1] + r[W-2](c) = A c + B, composed over the tile's chunks
+      float tA = 1.0f, tB = 0.0f;
+#pragma unroll
+      for (int cc = 0; cc < kChunks; ++cc) {
+        const int l = cc * kDwW + kDwW - 2;
+        const float x30 = readlane(x, l), y30 = readlane(y, l), v31 = readlane(vg, l + 1);
+        const f32x2 g0 = g0_lds[u][cc];
+        const bool f30 = ((via0_mask >> l) & 1) != 0;
+        const float mA = f30 ? x30 * g0.x : 0.0f;
+        const float mB = v31 + (f30 ? fmaf(x30, g0.y, y30) : y30);
+        if (cc == 0) {
+          if (lane == 0) map_lds[u] = f32x2{mA, mB};
+          tA = mA;
+          tB = mB;
+        } else {
+          tB = fmaf(mA, tB, mB);
+          tA = mA * tA;
+        }
+      }
+      const bool publisher = cur_live && lane == 0 && cur.tile != a.skip_publish;
+      status_store(st, publisher ? (uint32_t)(cur.tile * sizeof(uint64_t)) : kNoOffset,
+                   pack_map(tA, tB));
+    }
+
+    // (5) finish the oldest deferred tile (nothing is stored while the ring fills)
     {
       const float c_tile = tile_carry;
       float c_chunk = c_tile;  // the carry into this lane's chunk
@@ -618,19 +621,19 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
     held_B[hs] = B;
     have[hs] = cur_live;
 
-    // (5) wave 0: load the predecessor words of the tile finished in the next step, before
-    // the refill (vector loads complete in issue order); lanes before the row start and all
-    // other waves read 0, the constant map 0 (the zero initial state)
+    // (6) the look-back wave: load the predecessor words of the tile finished in the next
+    // step, before the refill (vector loads complete in issue order); lanes before the row
+    // start and all other waves read 0, the constant map 0 (the zero initial state)
     {
       const DwSlot& nxt = ring[(u + 3) % N];
       const bool nxt_live = nxt.tile < ntiles;
       const int64_t q = nxt.tile - 64 + lane;
       const int64_t nseg = nxt.tile & seg_mask;
-      const bool mine = w == 0 && nxt_live && nseg > 0 && q >= nxt.tile - nseg;
+      const bool mine = w == kLookWave && nxt_live && nseg > 0 && q >= nxt.tile - nseg;
       held_word = status_load(st, mine ? (uint32_t)(q * sizeof(uint64_t)) : kNoOffset);
     }
     pending[u] = claims.issue(st, leader && !claims_done);
-    // (6) refill the finished slot with the tile claimed two steps ago
+    // (7) refill the finished slot with the tile claimed two steps ago
     dw_setup<E, TW>(a, tax, tbx, fin, refill, ntiles, tpr_log2, w, lane);
     __builtin_amdgcn_sched_barrier(0);
   };
