@@ -815,8 +815,11 @@ def bench_fused(args):
 def bench_dimwise(args):
     """dw: dimwise_forward (the reference module's contraction scan) at the headline shape,
     B8 D1024 L65536; 3 N s bytes per call (read Ax and Bx, write Bx; Bh, Wq, Wk are
-    negligible). The reference's inputs (scans/contraction_scan.py:154-159)."""
+    negligible). The reference's inputs (scans/contraction_scan.py:154-159). Beside it, the
+    copy of the access pattern of the path the call takes: claimed 16 KiB tiles (tiled path,
+    the default at this size) or eight-wave rows (row kernel)."""
     import fpscan_amd
+    import fpscan_amd.ops as ops
 
     B, D, L = 8, 1024, 65536
     dtype = DTYPES[args.dtype or "bfloat16"]
@@ -833,11 +836,13 @@ def bench_dimwise(args):
     # in place: each call scans the previous call's output, which is the same work
     t = time_each(lambda: fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk), WARM_CALLS, args.iters)
     p50 = percentile(t, 0.5)
+    tiled = ops.dimwise_workspace_bytes(B, D, L, dtype) > 0
     entry = {"workload": "dw: dimwise_forward B8 D1024 L65536", "dtype": SHORT[dtype],
+             "path": "tiled" if tiled else "rows",
              "p50_ms": round(p50, 5), "gbps": round(3 * N * s / (p50 / 1e3) / 1e9, 1),
              "hbm_frac": round(3 * N * s / (p50 / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
-    # the copy of its access pattern (eight-wave rows, two 8 KiB rounds in flight, 2 reads +
-    # 1 write of the same tensor size), timed beside it
+    # the copy of the path's access pattern (2 reads + 1 write of the same tensor size), timed
+    # beside it
     import ctypes
 
     lib = ctypes.CDLL(os.path.join(os.path.dirname(fpscan_amd.__file__), "libfpscan_hip.so"))
@@ -845,27 +850,31 @@ def bench_dimwise(args):
     lib.fpscan_probe_copy.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, i64, i64,
                                       vp, ctypes.c_size_t, vp]
     lib.fpscan_probe_copy.restype = ctypes.c_int
+    lib.fpscan_probe_scratch_bytes.restype = ctypes.c_size_t
     del ax, bx0, bh, wq, wk, bx
     tensor_bytes = N * s
     src = torch.ones(2 * tensor_bytes, dtype=torch.uint8, device="cuda")
     dst = torch.empty(tensor_bytes, dtype=torch.uint8, device="cuda")
+    scratch = torch.zeros(lib.fpscan_probe_scratch_bytes(), dtype=torch.uint8, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
+    pattern = PROBE_PATTERNS["tiles"] if tiled else PROBE_ROWS8
 
     def probe():
-        st = lib.fpscan_probe_copy(PROBE_ROWS8, 2, 1, src.data_ptr(), dst.data_ptr(),
-                                   tensor_bytes, L * s, None, 0, stream)
+        st = lib.fpscan_probe_copy(pattern, 2, 1, src.data_ptr(), dst.data_ptr(), tensor_bytes,
+                                   L * s, scratch.data_ptr(), scratch.numel(), stream)
         if st != 0:
             raise RuntimeError(f"fpscan_probe_copy status {st}")
     e = _timed_entry(probe, 3 * tensor_bytes, args.iters)
-    entry["pattern_copy_rows8"] = {k: e[k] for k in ("p50_ms", "gbps", "hbm_frac")}
+    entry["pattern_copy_tiles" if tiled else "pattern_copy_rows8"] = {
+        k: e[k] for k in ("p50_ms", "gbps", "hbm_frac")}
     entry["of_pattern"] = round(entry["gbps"] / e["gbps"], 3)
-    del src, dst
+    del src, dst, scratch
     print(json.dumps(entry), flush=True)
     return entry
 
 
 PROBE_PATTERNS = {"tiles": 0, "blocks": 1, "rows": 2, "blocks_lookback": 3}  # fpscan_probe.h
-PROBE_ROWS8 = 4  # eight-wave rows, 8 KiB rounds, two in flight: dimwise_forward's pattern
+PROBE_ROWS8 = 4  # eight-wave rows, 8 KiB rounds, two in flight: dimwise's row kernel
 
 
 def bench_ceiling(args):

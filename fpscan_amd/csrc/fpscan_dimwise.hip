@@ -210,10 +210,16 @@ __global__ void __launch_bounds__(64 * NW) dimwise_rows(const DwArgs a) {
 // constant otherwise, and the chunk's outgoing carry v[W-1] + r[W-2](c) is an affine map of c.
 // A persistent grid claims 16 KiB tiles (two chunks of a 2-byte type, one of fp32) in memory
 // order (Claims, as the tiled row scan) and chains the tiles of a row by a decoupled
-// look-back over these maps: a tile reduces its chunks, selects, publishes the composed map at
-// once, and is finished D steps later from the carry its look-back found. In each step wave
-// 1 selects for the tile just reduced and publishes its map while wave 0 runs the look-back of
-// the tile finished next, so neither waits for the other.
+// look-back over these maps: a tile reduces its chunks, selects, publishes the composed map,
+// and is finished D steps later from the carry its look-back found. A step has two barriers:
+// after the reduce, the selection waves test the candidate groups (each wave a share of
+// them) while one other wave runs the look-back of the tile finished in this step and makes
+// the claims; after the second barrier wave 1 combines the selection and publishes the map
+// while the other waves finish the deferred tile, whose terms were made D steps earlier.
+// Measured on MI355X (B8 D1024 L65536, the same buffers, alternated): the combine and publish
+// before that barrier, with a third one between selection and combine, cost bf16 0.581 ms
+// against 0.552 now; 8 KiB tiles (one chunk, two workgroups per CU) 0.612 -- their copy
+// pattern alone reaches 5.77 TB/s against 6.28 for 16 KiB tiles (FPSCAN_PROBE_TILES8).
 //
 // Workspace: as the tiled row scan's ([0, ntiles) tile status, [ntiles] wait overruns, claim
 // counters after it).
@@ -722,9 +728,17 @@ int run_dw(const DwArgs& a, int P, hipStream_t stream) {
   return FPSCAN_ERR_SEQLEN;
 }
 
-// Tiled path. Below this many bytes per tensor the row kernel is used: the tiled launch's fixed
-// cost (status clear, start-up claims, filling and draining the ring) is then a large share.
-constexpr int64_t kDwTiledMinBytes = 512ll << 20;
+// Tiled path, taken automatically for rows of at least 64 KiB and at least 256 MiB per tensor.
+// Measured on MI355X (same buffers, alternated, median of 5, us, row kernel against tiled):
+// 128 KiB rows bf16 B8 D1024 L65536 623 / 561, 512 MiB 319 / 289, 256 MiB 161 / 158, 128 MiB
+// 75 / 89; fp32 L32768 1 GiB 583 / 517, 256 MiB 148 / 143; 64 KiB rows bf16 (16, 1024,
+// 32768) 614 / 558, (8, 1024, 32768) 300 / 289, fp32 (16, 1024, 16384) 582 / 516. Shorter
+// rows stream well in the row kernel: 32 KiB rows bf16 (16, 1024, 16384) 277 / 288, (32,
+// 1024, 16384) 564 / 558; 16 KiB rows (64, 1024, 8192) 528 / 556. Below 256 MiB the tiled
+// launch's fixed cost (status clear, start-up claims, filling and draining the ring) is a
+// large share.
+constexpr int64_t kDwTiledMinBytes = 256ll << 20;
+constexpr int64_t kDwTiledMinRowBytes = 64ll << 10;
 
 struct DwTilePlan {
   bool use;
@@ -739,7 +753,7 @@ DwTilePlan plan_dw_tiles(int64_t rows, int64_t seqlen, int size) {
   if (tiling == 1 || seqlen < 2 * kDwChunk) return t;
   const int64_t bytes = rows * seqlen * size;  // below 2^48: no wrap
   if (bytes >= ((int64_t)1 << 32)) return t;  // one buffer range per tensor
-  if (tiling == 0 && bytes < kDwTiledMinBytes) return t;
+  if (tiling == 0 && (bytes < kDwTiledMinBytes || seqlen * size < kDwTiledMinRowBytes)) return t;
   const int64_t tpr = seqlen * size / (kDwTileWaves * 1024);
   while (((int64_t)1 << t.tpr_log2) < tpr) ++t.tpr_log2;
   t.ntiles = rows << t.tpr_log2;

@@ -15,8 +15,8 @@
 //           rounds in flight (the pattern of the row-streaming scan with 16 waves per row).
 //   ROWS8   one 512-thread workgroup per row, 8 KiB rounds, two in flight (the pattern of
 //           dimwise_forward's row kernel and of the row scans with eight waves per row).
-//   TILES8  as TILES with 8 KiB tiles and 512-thread workgroups, two per CU (the pattern of
-//           dimwise_forward's tiled path for 2-byte types).
+//   TILES8  as TILES with 8 KiB tiles and 512-thread workgroups, two per CU: the tile size
+//           the tiled kernels do not use, for comparison with TILES.
 //   BLOCKS_LOOKBACK  256-thread blocks of 16 KiB tiles in memory order, each waiting before its
 //           stores until every earlier tile of its row has loaded its data: the wait a
 //           single-pass scan in memory order needs.

@@ -254,6 +254,16 @@ def dimwise_groups(seqlen: int) -> int:
     return int(_load_extension().dimwise_groups(int(seqlen)))
 
 
+_DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+
+def dimwise_workspace_bytes(batch: int, dim: int, seqlen: int, dtype: torch.dtype) -> int:
+    """Workspace dimwise_forward allocates for this problem: nonzero exactly when it takes the
+    tiled path (which depends on ``set_tiling``), 0 when it takes the row kernel."""
+    return int(_load_extension().dimwise_workspace_bytes(int(batch), int(dim), int(seqlen),
+                                                         _DTYPE_CODE[dtype]))
+
+
 def set_launch_override(waves_per_row: int = 0, ring_depth: int = 0) -> None:
     """Tuning hook: force the number of waves per row and the per-wave ring depth of the
     long-row kernels (0 restores the built-in choice). Process-wide."""

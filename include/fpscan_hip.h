@@ -213,8 +213,8 @@ int fpscan_dimwise_fwd(const void* gates, void* tokens, const void* bh, const vo
                        const void* wk, int64_t batch, int64_t dim, int64_t seqlen, int dtype,
                        void* stream);
 
-/* fpscan_dimwise_fwd with a workspace: problems of at least 512 MiB per tensor with seqlen
- * 8192..65536 (every chunk 32 groups of 128) then take a tiled path, whose 16 KiB tiles are
+/* fpscan_dimwise_fwd with a workspace: problems of 256 MiB to 4 GiB per tensor with rows of
+ * at least 64 KiB (seqlen * itemsize) then take a tiled path, whose 16 KiB tiles are
  * claimed in memory order and chained by a look-back over the chunks' carry maps (the carry
  * enters a chunk affinely: only group 0 depends on it, and the selection does not), with
  * bounded waits as the tiled scans'. It needs fpscan_dimwise_workspace_bytes() bytes, 8-byte
@@ -222,7 +222,8 @@ int fpscan_dimwise_fwd(const void* gates, void* tokens, const void* bh, const vo
  * smaller one the call takes the row kernel. Same results up to fp32 rounding order, except
  * where the selection finds no score above the initial one (non-finite or |score| >= 1e10
  * inputs): the non-finite outputs may then differ in kind. fpscan_set_tiling applies (1: row
- * kernel only; 2: tiled for any seqlen of 8192 or more). The reference's dimwise_forward takes
+ * kernel only; 2: tiled for any seqlen of 8192 or more, where every chunk is 32 groups of 128,
+ * below 4 GiB per tensor). The reference's dimwise_forward takes
  * no workspace: the torch binding allocates it from the caching allocator. */
 int fpscan_dimwise_fwd_ws(const void* gates, void* tokens, const void* bh, const void* wq,
                           const void* wk, int64_t batch, int64_t dim, int64_t seqlen, int dtype,

@@ -29,7 +29,8 @@ extern "C" {
                                  two in flight (dimwise_forward's row kernel; the row scans'
                                  eight-wave rows) */
 #define FPSCAN_PROBE_TILES8 5 /* as FPSCAN_PROBE_TILES with 8 KiB tiles and 512-thread
-                                 workgroups (dimwise_forward's tiled path, 2-byte types) */
+                                 workgroups, two per CU (a tile size the tiled kernels do not
+                                 use, for comparison) */
 
 #define FPSCAN_PROBE_OK 0
 #define FPSCAN_PROBE_ERR_ARG 1    /* unknown pattern or read/write count, bad size, alignment,

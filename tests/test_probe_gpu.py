@@ -28,8 +28,8 @@ def lib():
     return lib
 
 
-@pytest.mark.parametrize("pattern", [0, 1, 2, 3, 4],
-                         ids=["tiles", "blocks", "rows", "lookback", "rows8"])
+@pytest.mark.parametrize("pattern", [0, 1, 2, 3, 4, 5],
+                         ids=["tiles", "blocks", "rows", "lookback", "rows8", "tiles8"])
 @pytest.mark.parametrize("nr,nw", [(2, 1), (3, 2)], ids=["2r1w", "3r2w"])
 @pytest.mark.parametrize("tensor_kib,row_kib", [(16, 16), (4096, 128), (49152, 256)])
 def test_probe_moves_every_byte(lib, pattern, nr, nw, tensor_kib, row_kib):
