@@ -276,19 +276,6 @@ struct DwSlot {
 // outside every such range: loads from it return 0 and stores to it are dropped.
 constexpr uint32_t kDwNoOffset = 0xfffffff0u;
 
-// Claim groups over rows, as RowGroups, with each group's first tile computed where it is
-// used: the index is made opaque, so the compiler does not precompute all nine bounds ahead
-// of the kernel's loop and hold them (18 scalar registers) across it.
-struct DwRowGroups {
-  int64_t rows;
-  int tpr_log2;
-  __device__ int64_t first(int g) const {
-    g = __builtin_amdgcn_readfirstlane(g);  // uniform (one lane claims)
-    asm volatile("" : "+s"(g));
-    return ((int64_t)g * rows / kClaimGroups) << tpr_log2;
-  }
-};
-
 template <class E>
 __device__ __forceinline__ float widen_par(uint32_t bits) {
   if constexpr (E::kSize == 4) {
@@ -373,9 +360,9 @@ dimwise_tiles(const DwTileArgs a, uint64_t* __restrict__ status, const int tpr_l
   const float kInit = round_t<E>(-1e10f);
 
   const int64_t kBubble = ntiles, kDone = ntiles + 1;
-  Claims<DwRowGroups> claims{(uint32_t)((ntiles + kCounterStride) * sizeof(uint64_t)),
+  Claims<RowGroupsLazy> claims{(uint32_t)((ntiles + kCounterStride) * sizeof(uint64_t)),
                              reinterpret_cast<const uint32_t*>(status + ntiles + kCounterStride),
-                             DwRowGroups{ntiles >> tpr_log2, tpr_log2},
+                             RowGroupsLazy{ntiles >> tpr_log2, tpr_log2},
                              (int)(blockIdx.x % kClaimGroups)};
   Claim pending[N];
 #pragma unroll

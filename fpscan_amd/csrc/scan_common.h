@@ -394,11 +394,26 @@ __global__ void __launch_bounds__(256) clear_status(uint64_t* __restrict__ statu
 }
 
 // Claim groups over rows: group g holds rows [g rows / 8, (g + 1) rows / 8), each of
-// 2^tpr_log2 tiles (the row scan's tiled kernel).
+// 2^tpr_log2 tiles (the probes' tiles).
 struct RowGroups {
   int64_t rows;
   int tpr_log2;
   __device__ int64_t first(int g) const { return ((int64_t)g * rows / kClaimGroups) << tpr_log2; }
+};
+
+// RowGroups with each group's first tile computed where it is used: the index is made opaque,
+// so the compiler does not precompute all nine bounds ahead of a kernel's loop and hold them
+// (18 scalar registers) across it. For kernels short of scalar registers (the tiled dimwise
+// kernel: its spills to VGPR lanes cost it; the tiled row scan measured the same either way).
+// g is uniform (one lane claims).
+struct RowGroupsLazy {
+  int64_t rows;
+  int tpr_log2;
+  __device__ int64_t first(int g) const {
+    g = __builtin_amdgcn_readfirstlane(g);
+    asm volatile("" : "+s"(g));
+    return ((int64_t)g * rows / kClaimGroups) << tpr_log2;
+  }
 };
 
 // Tile claims, made by one lane per workgroup. One counter at one address serialises at the
