@@ -7,7 +7,9 @@ number, so a failure names a case that reruns identically:
   reverse and the fused backward;
 * row scans through the C ABI on padded strides (the padding must come back untouched);
 * channel-last scans (any seqlen, dim a multiple of the 16-byte vector), every path;
-* the fused softplus gates, forward, reverse and backward (grad_z, grad_rate, grad_tokens).
+* the fused softplus gates, forward, reverse and backward (grad_z, grad_rate, grad_tokens);
+* dimwise_forward at any supported seqlen on the automatic, row and tiled paths, on keys
+  spaced so that the first-maximum selection is unambiguous in every dtype.
 The bar is the tests' normwise one (north star: 1e-5 fp32, 5e-3 fp16, 2e-2 bf16); grad_rate,
 a sum over batch and seqlen per dim, gets max(bar, 1e-4) as in test_softplus_gpu.py.
 """
@@ -29,7 +31,7 @@ pytestmark = [
     pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a HIP device (MI355X)"),
 ]
 
-CASES = 96
+CASES = 108
 MAX_ELEMENTS = 1 << 22
 CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -209,7 +211,31 @@ def _softplus(rng, gen, dtype):
     assert err <= max(NORM_TOL[dtype], 1e-4), f"{desc}: grad_rate normwise error {err:.3e}"
 
 
-KINDS = [_rows_api, _rows_api, _rows_abi_strided, _channel_last, _softplus]
+def _dimwise(rng, gen, dtype):
+    seqlens = sorted(oracle.DIMWISE_GEOMETRY)
+    L = rng.choice(seqlens + [s for s in seqlens if s >= 8192])  # the tiled seqlens twice
+    B, D = rng.randint(1, 3), rng.randint(1, 24)
+    tiling = rng.choice([0, 1, 2, 2])
+    sign = rng.choice([1.0, -1.0])
+    desc = f"dimwise ({B}, {D}, {L}) {dtype} tiling {tiling} sign {sign}"
+    W, P, C = oracle.DIMWISE_GEOMETRY[L]
+    ax = 0.99 + 0.01 * torch.rand(B, D, L, generator=gen)
+    bx = sign * (0.5 + 0.5 * torch.rand(B, D, L, generator=gen)) / P
+    ranks = torch.rand(B, D, W, generator=gen).argsort(dim=-1).argsort(dim=-1).double()
+    bh = torch.randn(B, D, W * C, generator=gen) / (W * C)
+    bh[:, :, :W] = ((-1.0 + 2.0 * ranks / max(W - 1, 1)) / 4).float()
+    wq = 0.01 * torch.rand(D, generator=gen)
+    wk = 0.01 * torch.rand(D, generator=gen)
+    t = [v.to(dtype).contiguous() for v in (ax, bx, bh, wq, wk)]
+    want = oracle.dimwise_f64(*t)
+    dev = [v.to(DEVICE) for v in t]
+    with paths(tiling):
+        fpscan_amd.dimwise_forward(*dev)
+        torch.cuda.synchronize()
+    _assert_within({"dimwise": oracle.normwise_error(dev[1].cpu(), want)}, dtype, desc)
+
+
+KINDS = [_rows_api, _rows_api, _rows_abi_strided, _channel_last, _softplus, _dimwise]
 
 
 @pytest.mark.parametrize("case", range(CASES))
