@@ -232,3 +232,27 @@ def test_headline_shape_b8_d1024_l65536(dtype, mode):
         fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk)
     check(sel(bx), want, dtype, f"dimwise headline {dtype} tiling {mode}")
     assert fpscan_amd.lookback_overruns() == before
+
+
+@pytest.mark.parametrize("B", [15, 16], ids=["3.75GiB-tiled", "4GiB-rows"])
+def test_tensors_near_4_gib(B):
+    """fp32 (B, 1024, 65536): 3.75 GiB per tensor takes the tiled path, whose tile offsets are
+    32-bit byte offsets into one buffer range per tensor; 4 GiB takes the row kernel. Sampled
+    rows, the last ones included, against the oracle."""
+    D, L = 1024, 65536
+    tiled = ops.dimwise_workspace_bytes(B, D, L, torch.float32) > 0
+    assert tiled == (B * D * L * 4 < (1 << 32))
+    gen = torch.Generator(device=DEVICE).manual_seed(B)
+    ax = 0.99 + 0.01 * torch.rand(B, D, L, generator=gen, device=DEVICE)
+    bx = (0.5 + 0.5 * torch.rand(B, D, L, generator=gen, device=DEVICE)) / 128
+    bh = torch.randn(B, D, 512, generator=gen, device=DEVICE) / 512
+    wq = 0.01 * torch.rand(D, generator=gen, device=DEVICE)
+    wk = 0.01 * torch.rand(D, generator=gen, device=DEVICE)
+    rows = [0, 1, B * D // 2, B * D - 2, B * D - 1]
+    sel = lambda t: t.reshape(B * D, -1)[rows].reshape(1, len(rows), -1).cpu()  # noqa: E731
+    want = oracle.dimwise_f64(sel(ax), sel(bx), sel(bh), wq.cpu()[[r % D for r in rows]],
+                              wk.cpu()[[r % D for r in rows]])
+    before = fpscan_amd.lookback_overruns()
+    fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk)
+    check(sel(bx), want, torch.float32, f"dimwise fp32 B{B} (tiled {tiled})")
+    assert fpscan_amd.lookback_overruns() == before
