@@ -456,7 +456,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("set_tiling", [](int mode) {
     TORCH_CHECK(fpscan_set_tiling(mode) == FPSCAN_OK, "tiling mode must be 0, 1 or 2");
   }, "path selection: 0 automatic, 1 no tiled look-back (rows streamed; channel-last one pass "
-     "or segments), 2 tiled whenever possible",
+     "or segments; dimwise's row kernel), 2 tiled whenever possible",
         pybind11::arg("mode"));
   m.def("workspace_bytes", &fpscan_workspace_bytes, pybind11::arg("batch"),
         pybind11::arg("dim"), pybind11::arg("seqlen"), pybind11::arg("dtype"),

@@ -299,7 +299,8 @@ def set_lookback_test_hook(unpublished_tile: int = -1, spin_limit: int = 0) -> N
 
 
 def set_tiling(mode: int = 0) -> None:
-    """Path selection (process-wide) for long rows and channel-last scans: 0 automatic,
-    1 no tiled look-back (rows streamed; channel-last one pass per strip or segments),
-    2 tiled (persistent grid with look-back) whenever the shape allows."""
+    """Path selection (process-wide) for long rows, channel-last scans and dimwise_forward:
+    0 automatic, 1 no tiled look-back (rows streamed; channel-last one pass per strip or
+    segments; dimwise's row kernel), 2 tiled (persistent grid with look-back) whenever the
+    shape allows."""
     _load_extension().set_tiling(int(mode))

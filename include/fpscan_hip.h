@@ -266,14 +266,15 @@ int fpscan_set_lookback_test_hook(int64_t unpublished_tile, int spin_limit);
 int fpscan_set_launch_override(int waves_per_row, int ring_depth);
 
 /* Path selection for tests and tuning (a test hook); process-wide, not synchronised with
- * calls in flight. 0: automatic (rows: tiled for problems
- * of at least 512 MiB per tensor, backward from 256 MiB with rows of 64 KiB or more, rows
- * of exactly 16 sub-chunks from 1 GiB except the 2-byte backward, which streams them;
- * channel-last: tiled look-back when one pass per strip lacks strips or from 512 MiB per
- * tensor), 1: no tiled look-back (rows streamed; channel-last one
- * pass or segments), 2: tiled whenever possible (rows with 16..1024 sub-chunks; any
- * channel-last problem whose 130-row tile fits a 2 GiB buffer range). Tiled paths need the
- * workspace. No reference counterpart. */
+ * calls in flight. 0: automatic (rows: tiled for problems of at least 512 MiB per tensor,
+ * backward from 256 MiB with rows of 64 KiB or more, rows of exactly 16 sub-chunks from 1 GiB
+ * except the 2-byte backward, which streams them; channel-last: tiled look-back when one pass
+ * per strip lacks strips or from 512 MiB per tensor; dimwise: tiled for rows of 64 KiB or
+ * more from 256 MiB per tensor), 1: no tiled look-back (rows streamed; channel-last one pass
+ * or segments; dimwise's row kernel), 2: tiled whenever possible (rows with 16..1024
+ * sub-chunks; any channel-last problem whose 130-row tile fits a 2 GiB buffer range; dimwise
+ * seqlen 8192..65536 below 4 GiB per tensor). Tiled paths need the workspace. No reference
+ * counterpart. */
 int fpscan_set_tiling(int mode);
 
 #ifdef __cplusplus
