@@ -10,7 +10,8 @@
   reference has no cross-workgroup wait (full_scan.cu:77-175 keeps every carry in one block).
 * Long runs: hundreds of back-to-back tiled calls (row and channel-last kernels) at the
   headline size and the one-GPU share, outputs filled with NaN before each call, so that a tile
-  that is dropped or a wait that gives up in one call in a hundred is seen.
+  that is dropped or a wait that gives up in one call in a hundred is seen; the tiled dimwise
+  kernel in place, its input restored before each call and every output equal to the first.
 * HIP graph capture through the torch binding is refused with a RuntimeError before anything
   is launched (the capture is begun and ended with the runtime's own calls, no graph is
   instantiated).
@@ -356,6 +357,42 @@ def test_repeated_channel_last_tiled_calls_drop_no_tile(batch, op, calls):
     assert not bool(nan_seen), "an output element was left unwritten or poisoned"
     for a, b in zip(outs, first):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype,calls", [(torch.bfloat16, 200), (torch.float32, 100)],
+                         ids=["bf16", "f32"])
+def test_repeated_dimwise_tiled_calls_drop_no_tile(dtype, calls):
+    """dimwise_forward's tiled path at (8, 1024, 65536), in place: Bx is restored from the same
+    input before each call, and every call's output must equal the first bit for bit (a tile
+    left unwritten keeps its input, a wait that gave up leaves NaN) with no wait given up."""
+    B, D, L = 8, 1024, 65536
+    assert ops.dimwise_workspace_bytes(B, D, L, dtype) > 0, "the tiled path is the default here"
+    G = fpscan_amd.dimwise_groups(L)
+    gen = torch.Generator(device=DEVICE).manual_seed(23)
+    ax = (0.99 + 0.01 * torch.rand(B, D, L, generator=gen, device=DEVICE)).to(dtype)
+    bx0 = (torch.randn(B, D, L, generator=gen, device=DEVICE) / G).to(dtype)
+    bh = (torch.randn(B, D, G, generator=gen, device=DEVICE) / G).to(dtype)
+    wq = (0.01 * torch.rand(D, generator=gen, device=DEVICE)).to(dtype)
+    wk = (0.01 * torch.rand(D, generator=gen, device=DEVICE)).to(dtype)
+    bits = torch.int16 if dtype != torch.float32 else torch.int32
+    bx = torch.empty_like(bx0)
+    differs = torch.zeros((), dtype=torch.bool, device=DEVICE)
+    first = None
+    torch.cuda.synchronize()
+    before = fpscan_amd.lookback_overruns()
+    for i in range(calls):
+        bx.copy_(bx0)
+        fpscan_amd.dimwise_forward(ax, bx, bh, wq, wk)
+        if i == 0:
+            first = bx.clone()
+        else:
+            differs |= (bx.view(bits) != first.view(bits)).any()
+    torch.cuda.synchronize()
+    after = fpscan_amd.lookback_overruns()
+    assert after == before, f"{after - before} look-back waits gave up in {calls} calls"
+    assert not bool(differs), "a call's output differs from the first call's"
+    assert not torch.isnan(first).any()
+    assert not torch.equal(first.view(bits), bx0.view(bits))
 
 
 # ------------------------------------------------------------------ graph capture is refused
