@@ -868,6 +868,12 @@ def bench_dimwise(args):
     entry["pattern_copy_tiles" if tiled else "pattern_copy_rows8"] = {
         k: e[k] for k in ("p50_ms", "gbps", "hbm_frac")}
     entry["of_pattern"] = round(entry["gbps"] / e["gbps"], 3)
+    if tiled:
+        # for comparison, the same copy in 8 KiB tiles with two 512-thread workgroups per CU
+        # (a tile of one 2-byte chunk), which the tiled kernel does not use
+        pattern = PROBE_TILES8
+        e8 = _timed_entry(probe, 3 * tensor_bytes, args.iters)
+        entry["pattern_copy_tiles8"] = {k: e8[k] for k in ("p50_ms", "gbps", "hbm_frac")}
     del src, dst, scratch
     print(json.dumps(entry), flush=True)
     return entry
@@ -875,6 +881,7 @@ def bench_dimwise(args):
 
 PROBE_PATTERNS = {"tiles": 0, "blocks": 1, "rows": 2, "blocks_lookback": 3}  # fpscan_probe.h
 PROBE_ROWS8 = 4  # eight-wave rows, 8 KiB rounds, two in flight: dimwise's row kernel
+PROBE_TILES8 = 5  # 8 KiB tiles, 512-thread workgroups: a tile size the kernels do not use
 
 
 def bench_ceiling(args):
