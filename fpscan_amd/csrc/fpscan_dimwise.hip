@@ -216,10 +216,10 @@ __global__ void __launch_bounds__(64 * NW) dimwise_rows(const DwArgs a) {
 // them) while one other wave runs the look-back of the tile finished in this step and makes
 // the claims; after the second barrier wave 1 combines the selection and publishes the map
 // while the other waves finish the deferred tile, whose terms were made D steps earlier.
-// Measured on MI355X (B8 D1024 L65536, the same buffers, alternated): the combine and publish
-// before that barrier, with a third one between selection and combine, cost bf16 0.581 ms
-// against 0.552 now; 8 KiB tiles (one chunk, two workgroups per CU) 0.612 -- their copy
-// pattern alone reaches 5.77 TB/s against 6.28 for 16 KiB tiles (FPSCAN_PROBE_TILES8).
+// Measured on MI355X (B8 D1024 L65536 bf16, the same buffers and timing, alternated): the
+// combine and publish before that barrier, with a third one between selection and combine,
+// 5 % slower; 8 KiB tiles (one chunk, two workgroups per CU) 11 % slower -- their copy
+// pattern alone is 8 % slower than that of 16 KiB tiles (FPSCAN_PROBE_TILES8).
 //
 // Workspace: as the tiled row scan's ([0, ntiles) tile status, [ntiles] wait overruns, claim
 // counters after it).
