@@ -216,10 +216,10 @@ __global__ void __launch_bounds__(64 * NW) dimwise_rows(const DwArgs a) {
 // them) while one other wave runs the look-back of the tile finished in this step and makes
 // the claims; after the second barrier wave 1 combines the selection and publishes the map
 // while the other waves finish the deferred tile, whose terms were made D steps earlier.
-// Measured on MI355X (B8 D1024 L65536 bf16, the same buffers and timing, alternated): the
-// combine and publish before that barrier, with a third one between selection and combine,
-// 5 % slower; 8 KiB tiles (one chunk, two workgroups per CU) 11 % slower -- their copy
-// pattern alone is 8 % slower than that of 16 KiB tiles (FPSCAN_PROBE_TILES8).
+// Measured on MI355X (B8 D1024 L65536 bf16, each against the kernel of its time in one
+// timing): the combine and publish before that barrier, with a third one between selection
+// and combine, 5 % slower; 8 KiB tiles (one chunk, two workgroups per CU) 6 % slower -- their
+// copy pattern alone is 8 % slower than that of 16 KiB tiles (FPSCAN_PROBE_TILES8).
 //
 // Workspace: as the tiled row scan's ([0, ntiles) tile status, [ntiles] wait overruns, claim
 // counters after it).
