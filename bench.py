@@ -824,11 +824,13 @@ def bench_dimwise(args):
     import fpscan_amd
     import fpscan_amd.ops as ops
 
-    B, D, L = 8, 1024, 65536
+    B, D, L = (int(v) for v in args.shape.split(",")) if args.shape else (8, 1024, 65536)
     dtype = DTYPES[args.dtype or "bfloat16"]
     s = torch.empty((), dtype=dtype).element_size()
     N = B * D * L
     G = fpscan_amd.dimwise_groups(L)
+    if G == 0:
+        raise SystemExit(f"bench.py: dimwise_forward does not support seqlen {L}")
     gen = torch.Generator(device="cuda").manual_seed(2)
     ax = (0.99 + 0.01 * torch.rand(B, D, L, generator=gen, device="cuda")).to(dtype)
     bx0 = (torch.randn(B, D, L, generator=gen, device="cuda") / G).to(dtype)
@@ -844,7 +846,7 @@ def bench_dimwise(args):
                   before=lambda: bx.copy_(bx0))
     p50 = percentile(t, 0.5)
     tiled = ops.dimwise_workspace_bytes(B, D, L, dtype) > 0
-    entry = {"workload": "dw: dimwise_forward B8 D1024 L65536", "dtype": SHORT[dtype],
+    entry = {"workload": f"dw: dimwise_forward B{B} D{D} L{L}", "dtype": SHORT[dtype],
              "path": "tiled" if tiled else "rows",
              "p50_ms": round(p50, 5), "gbps": round(3 * N * s / (p50 / 1e3) / 1e9, 1),
              "hbm_frac": round(3 * N * s / (p50 / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
@@ -860,6 +862,11 @@ def bench_dimwise(args):
     lib.fpscan_probe_scratch_bytes.restype = ctypes.c_size_t
     del ax, bx0, bh, wq, wk, bx
     tensor_bytes = N * s
+    # the probes copy whole 16 KiB tiles (rows of whole tiles for the row pattern), at most 4 GiB
+    if (tensor_bytes % (16 << 10) or tensor_bytes > (1 << 32)
+            or (not tiled and (L * s) % (16 << 10))):
+        print(json.dumps(entry), flush=True)
+        return entry
     src = torch.ones(2 * tensor_bytes, dtype=torch.uint8, device="cuda")
     dst = torch.empty(tensor_bytes, dtype=torch.uint8, device="cuda")
     scratch = torch.zeros(lib.fpscan_probe_scratch_bytes(), dtype=torch.uint8, device="cuda")
@@ -1047,6 +1054,9 @@ def main():
                     help="c2: the seqlens to sweep (default 32 .. 65536)")
     ap.add_argument("--batch", type=int, default=None,
                     help="c4cl/c5cl: override the batch (e.g. 1 for config 4's 8-GPU share)")
+    ap.add_argument("--shape", default=None,
+                    help="dw: batch,dim,seqlen instead of the headline 8,1024,65536 (with "
+                         "--tiling 1 or 2 to time one path)")
     ap.add_argument("--no-fp32", action="store_true",
                     help="c4: skip the fp32 step reported beside the bf16 headline")
     ap.add_argument("--no-rows", action="store_true",

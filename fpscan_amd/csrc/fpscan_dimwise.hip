@@ -715,16 +715,16 @@ int run_dw(const DwArgs& a, int P, hipStream_t stream) {
   return FPSCAN_ERR_SEQLEN;
 }
 
-// Tiled path, taken automatically for rows of at least 64 KiB and at least 256 MiB per tensor.
-// Measured on MI355X (same buffers, alternated, median of 5, us, row kernel against tiled):
-// 128 KiB rows bf16 B8 D1024 L65536 623 / 561, 512 MiB 319 / 289, 256 MiB 161 / 158, 128 MiB
-// 75 / 89; fp32 L32768 1 GiB 583 / 517, 256 MiB 148 / 143; 64 KiB rows bf16 (16, 1024,
-// 32768) 614 / 558, (8, 1024, 32768) 300 / 289, fp32 (16, 1024, 16384) 582 / 516. Shorter
-// rows stream well in the row kernel: 32 KiB rows bf16 (16, 1024, 16384) 277 / 288, (32,
-// 1024, 16384) 564 / 558; 16 KiB rows (64, 1024, 8192) 528 / 556. Below 256 MiB the tiled
+// Tiled path, taken automatically for rows of at least 64 KiB from 384 MiB per tensor.
+// Measured on MI355X with `bench.py --workload dw --shape B,D,L --tiling 1|2` (bf16, p50 ms,
+// row kernel / tiled): 128 KiB rows (8, 1024, 65536) 0.623 / 0.560, (2, 1024, 65536) 0.159 /
+// 0.163 (256 MiB: within 3 % either way over two runs; 384 MiB measured the tiles 8 % ahead),
+// (1, 1024, 65536) 0.076 / 0.092; 64 KiB rows (8, 1024, 32768) 0.304 / 0.299; 32 KiB rows
+// (16, 1024, 16384) 0.279 / 0.298, (32, 1024, 16384) 0.565 / 0.559; 16 KiB rows (64, 1024,
+// 8192) 0.528 / 0.558. Short rows stream well in the row kernel, and at small sizes the tiled
 // launch's fixed cost (status clear, start-up claims, filling and draining the ring) is a
 // large share.
-constexpr int64_t kDwTiledMinBytes = 256ll << 20;
+constexpr int64_t kDwTiledMinBytes = 384ll << 20;
 constexpr int64_t kDwTiledMinRowBytes = 64ll << 10;
 
 struct DwTilePlan {

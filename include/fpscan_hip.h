@@ -213,7 +213,7 @@ int fpscan_dimwise_fwd(const void* gates, void* tokens, const void* bh, const vo
                        const void* wk, int64_t batch, int64_t dim, int64_t seqlen, int dtype,
                        void* stream);
 
-/* fpscan_dimwise_fwd with a workspace: problems of 256 MiB to 4 GiB per tensor with rows of
+/* fpscan_dimwise_fwd with a workspace: problems of 384 MiB to 4 GiB per tensor with rows of
  * at least 64 KiB (seqlen * itemsize) then take a tiled path, whose 16 KiB tiles are
  * claimed in memory order and chained by a look-back over the chunks' carry maps (the carry
  * enters a chunk affinely: only group 0 depends on it, and the selection does not), with
@@ -270,7 +270,7 @@ int fpscan_set_launch_override(int waves_per_row, int ring_depth);
  * backward from 256 MiB with rows of 64 KiB or more, rows of exactly 16 sub-chunks from 1 GiB
  * except the 2-byte backward, which streams them; channel-last: tiled look-back when one pass
  * per strip lacks strips or from 512 MiB per tensor; dimwise: tiled for rows of 64 KiB or
- * more from 256 MiB per tensor), 1: no tiled look-back (rows streamed; channel-last one pass
+ * more from 384 MiB per tensor), 1: no tiled look-back (rows streamed; channel-last one pass
  * or segments; dimwise's row kernel), 2: tiled whenever possible (rows with 16..1024
  * sub-chunks; any channel-last problem whose 130-row tile fits a 2 GiB buffer range; dimwise
  * seqlen 8192..65536 below 4 GiB per tensor). Tiled paths need the workspace. No reference

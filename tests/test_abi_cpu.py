@@ -436,7 +436,7 @@ def test_dimwise_groups_and_validation(lib):
 def test_dimwise_workspace_and_validation(lib):
     """fpscan_dimwise_workspace_bytes: one status word per 16 KiB tile (two chunks of 4096
     elements of a 2-byte type, one of fp32) plus the counters when the tiled path is taken
-    (seqlen >= 8192, tensors below 4 GiB; automatically for rows of 64 KiB or more from 256
+    (seqlen >= 8192, tensors below 4 GiB; automatically for rows of 64 KiB or more from 384
     MiB per tensor), else 0;
     fpscan_dimwise_fwd_ws validates like fpscan_dimwise_fwd and checks the workspace's
     alignment before any launch."""
@@ -452,7 +452,8 @@ def test_dimwise_workspace_and_validation(lib):
         assert wb(8, 1024, 65536, 0) == (8192 * 16 + extra) * 8   # fp32: 16
         assert wb(16, 1024, 65536, 0) == 0                         # 4 GiB: row kernel
         assert wb(1, 1024, 65536, 2) == 0                          # 128 MiB: row kernel
-        assert wb(2, 1024, 65536, 2) == (2048 * 8 + extra) * 8    # 256 MiB: tiled
+        assert wb(2, 1024, 65536, 2) == 0                          # 256 MiB: row kernel
+        assert wb(3, 1024, 65536, 2) == (3072 * 8 + extra) * 8    # 384 MiB: tiled
         assert wb(8, 1024, 32768, 2) == (8192 * 4 + extra) * 8    # 64 KiB rows: tiled
         assert wb(32, 1024, 16384, 2) == 0                         # 32 KiB rows: row kernel
         assert wb(8, 1024, 4096, 2) == 0                           # one chunk per row
