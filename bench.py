@@ -30,7 +30,8 @@ Other workloads (``--workload``), for measurement runs: c1, c2 (fp32 seqlen swee
 and reverse), c3, c5 (plus its (batch, seqlen, dim) .mT variant), c4cl and c5cl (channel-last),
 dw (dimwise_forward, beside the copy of its access pattern), c4fused (fused softplus gates),
 ceiling (the library's copy probes with the scans' access patterns, beside the scans, row and
-channel-last) and share (the B1 share object alone). Multi-GPU runs are not part of this
+channel-last), share (the B1 share object alone) and rows (the row scans on any
+``--shape batch,dim,seqlen``; with ``--tiling 1`` or ``2`` it measures either path). Multi-GPU runs are not part of this
 build: ``--gpus N`` with N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -699,10 +700,18 @@ def bench_sweep(args):
 
 
 def bench_shape(args):
-    """c1 / c3 / c5: forward, reverse and backward kernels alone, p50 over --iters."""
+    """c1 / c3 / c5, or rows (any --shape B,D,L; bf16 unless --dtype): forward, reverse and
+    backward kernels alone, p50 over --iters. With --tiling 1 or 2, one path (the path
+    choice's crossovers are measured this way)."""
     import fpscan_amd
 
-    B, D, L, dname, dist = WORKLOADS[args.workload]
+    if args.workload == "rows":
+        if not args.shape:
+            raise SystemExit("bench.py: --workload rows needs --shape batch,dim,seqlen")
+        B, D, L = (int(v) for v in args.shape.split(","))
+        dname, dist = "bfloat16", "mamba"
+    else:
+        B, D, L, dname, dist = WORKLOADS[args.workload]
     dtypes = [DTYPES[args.dtype]] if args.dtype else (
         [torch.bfloat16, torch.float16] if args.workload == "c3" else [DTYPES[dname]])
     res = {"workload": args.workload, "shape": [B, D, L], "results": []}
@@ -1044,7 +1053,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw", "c4fused", "ceiling", "share"])
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5", "c4cl", "c5cl", "dw", "c4fused", "ceiling", "share", "rows"])
     ap.add_argument("--dtype", choices=list(DTYPES), default=None)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1055,8 +1064,8 @@ def main():
     ap.add_argument("--batch", type=int, default=None,
                     help="c4cl/c5cl: override the batch (e.g. 1 for config 4's 8-GPU share)")
     ap.add_argument("--shape", default=None,
-                    help="dw: batch,dim,seqlen instead of the headline 8,1024,65536 (with "
-                         "--tiling 1 or 2 to time one path)")
+                    help="dw, rows: batch,dim,seqlen (dw defaults to the headline 8,1024,65536; "
+                         "with --tiling 1 or 2 to time one path)")
     ap.add_argument("--no-fp32", action="store_true",
                     help="c4: skip the fp32 step reported beside the bf16 headline")
     ap.add_argument("--no-rows", action="store_true",

@@ -902,6 +902,8 @@ constexpr int kTileDefer = 2;
 // draining the four-tile pipeline), which dozens of tiles per workgroup amortise. Measured on
 // MI355X: at 128 MiB per tensor streaming wins (fp32 B2 D256 L65536 forward 72 us against
 // 87), at 512 MiB tiling wins by 6 % (fp32 B8 D1024 L16384) and at 1-2 GiB by 8-10 %.
+// Every shape quoted in these notes can be rerun with each path forced:
+// `python bench.py --workload rows --dtype D --shape B,D,L --tiling 1|2`.
 constexpr int64_t kTiledMinBytes = 512ll << 20;
 // The fused backward moves 5 tensors per tile instead of 3, so the same fixed cost is a smaller
 // share, and the streaming backward slows down on long rows (one workgroup per row streaming
