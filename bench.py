@@ -706,9 +706,7 @@ def bench_shape(args):
     import fpscan_amd
 
     if args.workload == "rows":
-        if not args.shape:
-            raise SystemExit("bench.py: --workload rows needs --shape batch,dim,seqlen")
-        B, D, L = (int(v) for v in args.shape.split(","))
+        B, D, L = args.shape
         dname, dist = "bfloat16", "mamba"
     else:
         B, D, L, dname, dist = WORKLOADS[args.workload]
@@ -833,7 +831,7 @@ def bench_dimwise(args):
     import fpscan_amd
     import fpscan_amd.ops as ops
 
-    B, D, L = (int(v) for v in args.shape.split(",")) if args.shape else (8, 1024, 65536)
+    B, D, L = args.shape or (8, 1024, 65536)
     dtype = DTYPES[args.dtype or "bfloat16"]
     s = torch.empty((), dtype=dtype).element_size()
     N = B * D * L
@@ -1082,6 +1080,15 @@ def main():
                     help="also run 5 device copies of a 1 GiB buffer: the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
+    if args.shape is not None:
+        try:
+            args.shape = tuple(int(v) for v in args.shape.split(","))
+        except ValueError:
+            args.shape = ()
+        if len(args.shape) != 3 or min(args.shape) < 1:
+            ap.error("--shape takes three positive integers: batch,dim,seqlen")
+    if args.workload == "rows" and args.shape is None:
+        ap.error("--workload rows needs --shape batch,dim,seqlen")
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
